@@ -1,0 +1,73 @@
+"""Builds ``libeagle4_amd.so``, the gfx950 kernels behind the ``eagle_harness`` host modules of this directory.
+
+Every ``csrc/*.hip`` file is compiled with hipcc for gfx950 into ``_build/`` (in parallel), then linked into
+``eagle_harness/kernels/libeagle4_amd.so``, where the host binding loads it. Runs offline: hipcc cross-compiles without
+a GPU. ``python eagle-4_amd/build.py`` builds from the command line.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+CSRC = ROOT / "csrc"
+BUILD = ROOT / "_build"
+LIBRARY = ROOT / "eagle_harness" / "kernels" / "libeagle4_amd.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops off: hipcc would otherwise pair fp32 adds / multiplies / FMAs into v_pk_*_f32 on its own.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build the gfx950 kernels)")
+
+
+def _compile(hipcc: str, src: Path) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+    return obj
+
+
+def build(jobs: int | None = None) -> Path:
+    """Compiles every kernel source and links the shared library; returns its path."""
+    hipcc = _hipcc()
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
+    with concurrent.futures.ThreadPoolExecutor(jobs) as pool:
+        objects = list(pool.map(lambda s: _compile(hipcc, s), sources))
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build())
+    sys.exit(0)

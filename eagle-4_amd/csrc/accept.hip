@@ -1,0 +1,225 @@
+// Greedy acceptance of a verified tree on gfx950: the target's argmax per row, the tree walk, the bs1 accept tail
+// and the row compaction (vllm/tree_accept.py:45-115, kernels/accept_tail.py:56-224).
+//
+// The argmax is the HBM-bound part (the logits of every verify row, 2.49 GB at 8192 x 151936 bf16): one workgroup
+// per row streams it with 16-byte loads and reduces (max, first index) in registers, then across the block. The walk
+// and the tail are a few hundred bytes per request, one thread per request.
+
+#include "common.h"
+
+namespace {
+
+// (value, index) with the first index on ties (torch.argmax); NaN compares as the largest value.
+E4_DEV bool better(float v, int64_t i, float bv, int64_t bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_kernel(const eagle4_argmax_args a) {
+  using S = typename T::storage;
+  const int row = blockIdx.x;
+  const S* p = static_cast<const S*>(a.logits) + static_cast<int64_t>(row) * a.stride_row;
+  constexpr int VEC = 16 / sizeof(S);
+  float bv = -INFINITY;
+  int64_t bi = INT64_MAX;
+  const bool aligned = (reinterpret_cast<uintptr_t>(p) % 16) == 0;
+  const int nvec = aligned ? a.vocab / VEC : 0;
+  for (int v = threadIdx.x; v < nvec; v += blockDim.x) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(v) * VEC);
+    const S* e = reinterpret_cast<const S*>(&raw);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      const float f = T::to_f32(e[i]);
+      const int64_t idx = static_cast<int64_t>(v) * VEC + i;
+      if (better(f, idx, bv, bi)) {
+        bv = f;
+        bi = idx;
+      }
+    }
+  }
+  for (int64_t i = static_cast<int64_t>(nvec) * VEC + threadIdx.x; i < a.vocab; i += blockDim.x) {
+    const float f = T::to_f32(p[i]);
+    if (better(f, i, bv, bi)) {
+      bv = f;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const float ov = __shfl_xor(bv, m, 64);
+    const int64_t oi = __shfl_xor(bi, m, 64);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float s_v[4];
+  __shared__ int64_t s_i[4];
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = bv;
+    s_i[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w)
+      if (better(s_v[w], s_i[w], bv, bi)) {
+        bv = s_v[w];
+        bi = s_i[w];
+      }
+    a.out[row] = bi;
+  }
+}
+
+// vllm/tree_accept.py:45-83 (_tree_accept_kernel): one thread per request.
+__global__ void accept_tree_kernel(const eagle4_accept_tree_args a) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= a.num_reqs) return;
+  const int64_t slot = e4::ld(a.idx_mapping, b);
+  const int64_t start = e4::ld(a.cu_num_logits, b);
+  const int64_t rows = e4::ld(a.cu_num_logits, b + 1) - start;
+  const int64_t limit = rows < a.width ? rows : a.width;
+  int node = 0, count = 0;
+  bool alive = rows > 0;
+  for (int step = 0; step < a.width; ++step) {
+    if (!alive) break;
+    const int64_t token = e4::ld(a.target, start + node);
+    a.sampled[b * a.stride_sampled + step] = token;
+    a.path[slot * a.stride_path + step] = node;
+    ++count;
+    int child = -1;
+    for (int r = 1; r < limit; ++r) {  // the lowest-index row that continues the walk (:78-79)
+      if (e4::ld(a.parents, slot, r) == node && e4::ld(a.drafted, start + r) == token) {
+        child = r;
+        break;
+      }
+    }
+    alive = child >= 0;
+    if (alive) node = child;
+  }
+  a.num_sampled[b] = count;
+  a.path_len[slot] = count;
+}
+
+// kernels/accept_tail.py:56-132 (_accept_tail_kernel), batch size 1, one thread.
+__global__ void accept_tail_kernel(const eagle4_accept_tail_args a) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const int width = a.width, depth = a.depth;
+  for (int d = 0; d < depth; ++d) a.accept_index[d] = -1;  // :79-80
+  int64_t last = e4::ld(a.retrieve_index, 0);
+  if (depth > 0) a.accept_index[0] = static_cast<int32_t>(last);
+  int64_t cur = 0, num = 0;
+  bool active = true;
+  for (int level = 1; level < depth && active; ++level) {  // :90-106
+    cur = e4::ld(a.retrieve_next_token, cur);
+    const int64_t target_token = e4::ld(a.target_predict, last);
+    int found = 0;
+    for (int sibling = 0; sibling < width && found == 0; ++sibling) {
+      const bool valid = cur != -1;
+      const int64_t safe = valid ? cur : 0;
+      const int64_t node = e4::ld(a.retrieve_index, safe);
+      const bool match = valid && e4::ld(a.candidates, safe) == target_token;
+      if (match) {
+        a.accept_index[num + 1] = static_cast<int32_t>(node);
+        num += 1;
+        last = node;
+      } else if (valid) {
+        cur = e4::ld(a.retrieve_next_sibling, safe);
+      }
+      found = match ? 1 : (valid ? 0 : -1);
+    }
+    active = found == 1;
+  }
+  // :110-113: accept lengths, the bonus token, the new length
+  const int64_t seq_len = e4::ld(a.seq_lens, 0);
+  a.accept_lens[0] = static_cast<int32_t>(num + 1);
+  e4::st(eagle4_itab{a.new_seq_lens, 0, 0, a.seq_lens.dtype, 0}, 0, 0, seq_len + num + 1);
+  a.bonus[0] = static_cast<int32_t>(e4::ld(a.target_predict, last));
+  // :115-123: the accepted path moved to the front (padding reads node 0's target)
+  for (int node = 0; node < width; ++node) {
+    int64_t value;
+    if (node < depth) {
+      const int64_t p = a.accept_index[node];
+      value = e4::ld(a.target_predict, p > 0 ? p : 0);
+    } else {
+      bool on_path = false;
+      for (int d = 0; d < depth && d <= num; ++d) on_path |= a.accept_index[d] == node;
+      value = on_path ? e4::ld(a.target_predict, node) : 0;
+    }
+    a.predict[node] = static_cast<int32_t>(value);
+  }
+  // :126-132: the KV slots to move
+  const int64_t row = e4::ld(a.req_pool_indices, 0);
+  for (int d = 0; d < depth; ++d) {
+    const bool keep = d <= num;
+    a.committed_slots[d] = keep ? e4::ld(a.req_to_token, row, seq_len + d) : 0;
+    a.accepted_slots[d] = keep ? e4::ld(a.out_cache_loc, a.accept_index[d]) : 0;
+  }
+}
+
+// kernels/accept_tail.py:190-206 (_compact_rows_kernel), 16-byte chunks when the row bytes allow.
+__global__ __launch_bounds__(256) void compact_rows_kernel(const eagle4_compact_rows_args a) {
+  const int row = blockIdx.y;
+  int64_t src_row = row;
+  if (row < a.depth) {
+    const int64_t p = e4::ld(a.accept_index, 0, row < a.depth - 1 ? row : a.depth - 1);
+    src_row = p > 0 ? p : 0;
+  }
+  const char* src = static_cast<const char*>(a.src) + src_row * a.src_stride;
+  char* dst = static_cast<char*>(a.dst) + static_cast<int64_t>(row) * a.dst_stride;
+  const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | a.row_bytes) & 15) == 0;
+  if (vec) {
+    for (int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * 16; i < a.row_bytes;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x * 16)
+      *reinterpret_cast<uint4*>(dst + i) = *reinterpret_cast<const uint4*>(src + i);
+  } else {
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < a.row_bytes;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+      dst[i] = src[i];
+  }
+}
+
+bool tab_ok(const eagle4_itab& t) { return t.ptr != nullptr && e4::is_index_dtype(t.dtype); }
+
+}  // namespace
+
+extern "C" int eagle4_argmax_rows(const eagle4_argmax_args* a, void* stream) {
+  if (a->rows == 0) return EAGLE4_OK;
+  if (a->vocab < 1 || a->out == nullptr) return EAGLE4_NOT_COVERED;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (a->dtype) {
+    case EAGLE4_BF16: argmax_kernel<e4::Bf16><<<a->rows, 256, 0, s>>>(*a); break;
+    case EAGLE4_F16: argmax_kernel<e4::F16><<<a->rows, 256, 0, s>>>(*a); break;
+    case EAGLE4_F32: argmax_kernel<e4::F32><<<a->rows, 256, 0, s>>>(*a); break;
+    default: return EAGLE4_NOT_COVERED;
+  }
+  return E4_LAUNCH_STATUS();
+}
+
+extern "C" int eagle4_accept_tree(const eagle4_accept_tree_args* a, void* stream) {
+  if (a->num_reqs == 0) return EAGLE4_OK;
+  if (!tab_ok(a->target) || !tab_ok(a->drafted) || !tab_ok(a->cu_num_logits) || !tab_ok(a->idx_mapping) ||
+      !tab_ok(a->parents) || a->width < 1)
+    return EAGLE4_NOT_COVERED;
+  accept_tree_kernel<<<e4::ceil_div(a->num_reqs, 64), 64, 0, static_cast<hipStream_t>(stream)>>>(*a);
+  return E4_LAUNCH_STATUS();
+}
+
+extern "C" int eagle4_accept_tail(const eagle4_accept_tail_args* a, void* stream) {
+  if (!tab_ok(a->target_predict) || !tab_ok(a->candidates) || !tab_ok(a->retrieve_index) ||
+      !tab_ok(a->retrieve_next_token) || !tab_ok(a->retrieve_next_sibling) || !tab_ok(a->seq_lens) ||
+      !tab_ok(a->out_cache_loc) || !tab_ok(a->req_to_token) || !tab_ok(a->req_pool_indices) || a->depth < 0)
+    return EAGLE4_NOT_COVERED;
+  accept_tail_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(*a);
+  return E4_LAUNCH_STATUS();
+}
+
+extern "C" int eagle4_compact_rows(const eagle4_compact_rows_args* a, void* stream) {
+  if (a->width == 0 || a->row_bytes == 0) return EAGLE4_OK;
+  if (!tab_ok(a->accept_index) || a->depth < 1) return EAGLE4_NOT_COVERED;
+  const int64_t chunks = (a->row_bytes + 16 * 256 - 1) / (16 * 256);
+  const dim3 grid(static_cast<unsigned>(chunks < 64 ? chunks : 64), a->width);
+  compact_rows_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(*a);
+  return E4_LAUNCH_STATUS();
+}

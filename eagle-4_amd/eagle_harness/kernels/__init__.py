@@ -1,0 +1,18 @@
+"""Kernels of the EAGLE-4 verify round on MI355X (gfx950). Raw tensors in, raw tensors out; no engine imports.
+
+==================  =====================================================================================
+module              what
+==================  =====================================================================================
+``arch``            which GPU runs the kernels (gfx950 only) and the feature predicates callers read
+``gdn_tree``        GDN tree tables: links -> parents, conv window codes, path table
+``gdn_tree_conv``   width-4 tree causal conv1d
+``gdn_tree_recurrence``  gated delta rule over the tree, per-node state snapshots
+``gdn_tree_records``     replay records and the accepted-path commit (records contract)
+``accept_tail``     bs1 greedy accept tail and row compaction
+``verify_prep``     tail-mask words
+``online_softmax``  where the online-softmax step lives (inside the HIP attention kernel)
+==================  =====================================================================================
+
+The kernels are compiled ahead of time into ``libeagle4_amd.so`` (``python eagle-4_amd/build.py``); ``_native`` binds
+it with ctypes.
+"""

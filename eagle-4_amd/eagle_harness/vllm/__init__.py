@@ -1,0 +1,2 @@
+"""Engine-free pieces of the reference's vLLM adapter that sit on the verify hot path: the tree-verify attention,
+the verify stage (tree masks, depths, window codes), the greedy tree walk and the accepted-path state commit."""

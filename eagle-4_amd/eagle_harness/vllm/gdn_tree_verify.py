@@ -1,0 +1,85 @@
+"""Accepted-path commit of the linear-attention state for vLLM hybrid targets (vllm/gdn_tree_verify.py:184-322),
+engine-free.
+
+vLLM keeps one recurrent-state slot per verify row (``slots[b, i]``) and the request's conv window in slot
+``slots[b, 0]``; the next step resumes from row / window offset ``num_accepted - 1``. The accepted rows of a tree are
+not a prefix of the verify rows, so :class:`LinearStateCommit` moves them into chain order: the window columns of
+the accepted path next to each other, and the last accepted row's recurrent state into row ``accepted - 1``. All
+layers move in one gfx950 launch per kind (``csrc/state_commit.hip``).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import Any
+
+import torch
+
+from eagle_harness.kernels import _native
+
+# A padded request's state slot (vLLM's null block); the chain kernels skip it too.
+NULL_BLOCK_ID = 0
+
+
+def _caches(layer: Any) -> tuple[torch.Tensor, torch.Tensor]:
+    """(window cache as [slots, dim, state_len], state pool) of a layer: a (conv, ssm) pair or an object with vLLM's
+    ``kv_cache`` = (conv, ssm), conv in either of vLLM's layouts ([slots, dim, len] or [slots, len, dim])."""
+    conv, ssm = layer if isinstance(layer, (tuple, list)) else (layer.kv_cache[0], layer.kv_cache[1])
+    return conv, ssm
+
+
+class LinearStateCommit:
+    """Moves the accepted rows of a tree round into chain order in GDN layers, all layers in one launch.
+
+    ``layers[i]``: layer ``i``'s (window cache viewed as [slots, dim, state_len], state pool [slots, ...]) pair (or a
+    layer object with ``kv_cache``); ``slots[i]``: its KV cache group's [reqs, S] int32 state-slot table.
+    """
+
+    def __init__(self, layers: Sequence[Any], slots: Sequence[torch.Tensor], device: torch.device):
+        self.num_layers = len(layers)
+        self.device = device
+        if not self.num_layers:
+            return
+        caches = [_caches(layer) for layer in layers]
+        first_conv, first_ssm = caches[0]
+        for conv, ssm in caches:
+            if conv.stride() != first_conv.stride() or conv.dtype != first_conv.dtype or ssm.stride() != first_ssm.stride():
+                raise ValueError("the linear-attention layers must share one state layout")
+            if ssm.dtype != first_ssm.dtype:
+                raise ValueError("the linear-attention layers must share one state dtype")
+        if any(s.dtype != torch.int32 for s in slots):
+            raise ValueError("state slots must be int32")
+        self.conv_dtype, self.ssm_dtype = first_conv.dtype, first_ssm.dtype
+        self.conv_strides = first_conv.stride()
+        self.dim = first_conv.shape[1]
+        self.ssm_stride, self.ssm_numel = first_ssm.stride(0), first_ssm[0].numel()
+        self.conv_ptrs = torch.tensor([c.data_ptr() for c, _ in caches], dtype=torch.uint64, device=device)
+        self.ssm_ptrs = torch.tensor([s.data_ptr() for _, s in caches], dtype=torch.uint64, device=device)
+        self.slots_ptrs = torch.tensor([s.data_ptr() for s in slots], dtype=torch.uint64, device=device)
+        self.slots_strides = torch.tensor([s.stride(0) for s in slots], dtype=torch.int64, device=device)
+        self._keep = (caches, list(slots))
+
+    def commit(self, idx_mapping: torch.Tensor, path: torch.Tensor, path_len: torch.Tensor) -> None:
+        """``path [state slots, W]`` / ``path_len [state slots]``: the accepted rows of each request, root first."""
+        if not self.num_layers:
+            return
+        args = _native.StateCommitArgs(
+            conv_ptrs=self.conv_ptrs.data_ptr(),
+            ssm_ptrs=self.ssm_ptrs.data_ptr(),
+            slots_ptrs=self.slots_ptrs.data_ptr(),
+            slots_strides=self.slots_strides.data_ptr(),
+            idx_mapping=_native.itab(idx_mapping),
+            path=_native.itab(path),
+            path_len=_native.itab(path_len),
+            conv_stride_slot=self.conv_strides[0],
+            conv_stride_dim=self.conv_strides[1],
+            conv_stride_tok=self.conv_strides[2],
+            ssm_stride_slot=self.ssm_stride,
+            ssm_numel=self.ssm_numel,
+            conv_dtype=_native.dtype_code(self.conv_dtype),
+            ssm_dtype=_native.dtype_code(self.ssm_dtype),
+            num_reqs=idx_mapping.shape[0],
+            layers=self.num_layers,
+            dim=self.dim,
+        )
+        _native.launch("eagle4_linear_state_commit", args, self.device)

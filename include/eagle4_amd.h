@@ -1,0 +1,323 @@
+/*
+ * eagle4_amd: the C ABI of the MI355X (gfx950) draft-tree verify kernels.
+ *
+ * One extern "C" entry per kernel family of eagle-harness 0.1.5's verify hot path. Every entry takes a pointer to a
+ * plain argument struct (raw device pointers, int64 element strides, sizes, dtype codes and flags; no torch types)
+ * and the HIP stream to launch on, and returns
+ *
+ *     EAGLE4_OK (0)            launched (or nothing to do),
+ *     EAGLE4_NOT_COVERED (-1)  a shape / dtype / layout these kernels do not cover; nothing was launched,
+ *     > 0                      a hipError_t from the launch.
+ *
+ * The convention is the reference's native ABI (eagle_harness/kernels/csrc/candidate.cu:563-570, 637-681, bound by
+ * eagle_harness/kernels/native.py:28-41): the host side validates arguments and raises on anything but 0. There is
+ * no fallback path: "not covered" is an error for the caller.
+ *
+ * The library never allocates and never synchronises: launches are asynchronous on `stream` (a hipStream_t), read
+ * and write only caller-owned memory, and can be captured in a HIP graph. The one scratch buffer (verify attention's
+ * split partials) is passed in by the caller; eagle4_verify_attention_workspace() gives its size.
+ *
+ * dtype codes follow the reference's (candidate.cu:566): 0 bfloat16, 1 float16, 2 float32; then 3 float8_e4m3fn
+ * (OCP), 4 int32, 5 int64, 6 uint8/bool.
+ */
+#ifndef EAGLE4_AMD_H_
+#define EAGLE4_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EAGLE4_OK 0
+#define EAGLE4_NOT_COVERED (-1)
+
+#define EAGLE4_BF16 0
+#define EAGLE4_F16 1
+#define EAGLE4_F32 2
+#define EAGLE4_FP8_E4M3 3
+#define EAGLE4_I32 4
+#define EAGLE4_I64 5
+#define EAGLE4_U8 6
+
+/* An integer table on the device: element [i, j] is at ptr + i * s0 + j * s1 (elements), dtype EAGLE4_I32 or
+ * EAGLE4_I64. A null ptr means "absent" where an argument is optional. */
+typedef struct eagle4_itab {
+  const void* ptr;
+  int64_t s0;
+  int64_t s1;
+  int32_t dtype;
+  int32_t reserved;
+} eagle4_itab;
+
+/* ---- verify stage: vllm/verify_layout.py:31-86 (_stage_tree_kernel), :147-185 (VerifyStage.stage) ---------------- */
+typedef struct eagle4_stage_tree_args {
+  eagle4_itab parents;         /* [slots, W] parent row of each verify row (row 0: -1) */
+  eagle4_itab idx_mapping;     /* [R] request state slot of each batch row */
+  eagle4_itab query_start_loc; /* [R + 1] */
+  eagle4_itab cu_num_logits;   /* [R + 1] */
+  int64_t* positions;          /* [tokens] chain positions in, depth positions out */
+  int32_t* stage_parents;      /* [R, W] contiguous */
+  int32_t* stage_anc;          /* [R, 3, W] contiguous */
+  int64_t* stage_mask;         /* [R, W] contiguous: bit j set iff row j is an ancestor of the row or the row */
+  int32_t* context_lens;       /* [R] */
+  int32_t* slot_parents;       /* [slots, W] contiguous */
+  int32_t* slot_depths;        /* [slots, W] contiguous */
+  int32_t num_reqs;
+  int32_t width; /* W <= 64 */
+  int32_t tree;  /* 0: stage every request as a chain */
+  int32_t reserved;
+} eagle4_stage_tree_args;
+int eagle4_stage_tree(const eagle4_stage_tree_args* args, void* stream);
+
+/* ---- GDN tree tables: kernels/gdn_tree.py:93-237 (gdn_tree_ancestors, _gdn_tree_paths) ---------------------------- */
+typedef struct eagle4_ancestors_args {
+  eagle4_itab next_token;         /* [batch, >= width] first-child links */
+  eagle4_itab next_sibling;       /* [batch, >= width] next-sibling links */
+  eagle4_itab parent_token;       /* [batch, >= width] written: parent of every node */
+  eagle4_itab conv_state_indices; /* [batch] */
+  eagle4_itab query_start_loc;    /* [batch + 1], read only with paths */
+  int32_t* ancestors;             /* [batch, 3, width] contiguous */
+  int32_t* paths;                 /* [batch, width, 2 + width], unit last stride; null: no path table */
+  int64_t stride_paths_seq;
+  int64_t stride_paths_path;
+  int32_t batch;
+  int32_t width; /* <= 1024; < 256 with paths */
+  int32_t pad_slot_id;
+  int32_t reserved;
+} eagle4_ancestors_args;
+int eagle4_gdn_tree_ancestors(const eagle4_ancestors_args* args, void* stream);
+
+/* ---- tail-mask words: kernels/verify_prep.py:23-45 (tree_tail_words) -------------------------------------------- */
+typedef struct eagle4_tail_words_args {
+  const uint8_t* mask;       /* flattened [width, kv_len] bool / uint8 */
+  eagle4_itab committed_len; /* [1] */
+  int64_t* tail_bits;        /* [>= width] int64 */
+  int32_t width;             /* 1..64 */
+  int32_t reserved;
+} eagle4_tail_words_args;
+int eagle4_tree_tail_words(const eagle4_tail_words_args* args, void* stream);
+
+/* ---- GDN tree conv1d: kernels/gdn_tree_conv.py:402-497 (gdn_tree_conv1d_update) ----------------------------------- */
+typedef struct eagle4_conv_args {
+  const void* x; /* (batch, dim, seqlen) or (1, dim, tokens) with query_start_loc; 16-bit */
+  int64_t stride_x_seq, stride_x_dim, stride_x_token;
+  const void* weight; /* (dim, 4) */
+  int64_t stride_w_dim, stride_w_width;
+  const void* bias; /* (dim,) or null */
+  void* conv_state; /* [slots, dim, >= 3] any strides */
+  int64_t stride_cs_seq, stride_cs_dim, stride_cs_tok;
+  eagle4_itab conv_state_indices; /* [batch] */
+  eagle4_itab num_accepted;       /* [batch] or null */
+  eagle4_itab query_start_loc;    /* [batch + 1] or null */
+  void* window;                   /* [rows, steps, dim, >= 3] or null */
+  int64_t stride_win_seq, stride_win_step, stride_win_dim, stride_win_win;
+  eagle4_itab window_indices; /* [batch] */
+  const int32_t* ancestors;   /* [>= batch, 3, seqlen] contiguous */
+  void* out;                  /* like x */
+  int64_t stride_o_seq, stride_o_dim, stride_o_token;
+  int32_t batch, dim, seqlen, state_len;
+  int32_t pad_slot_id;
+  int32_t silu;
+  int32_t dtype;      /* x, weight, conv_state, out, window: EAGLE4_BF16 or EAGLE4_F16 */
+  int32_t bias_dtype; /* 0 / 1 / 2 */
+} eagle4_conv_args;
+int eagle4_gdn_tree_conv1d_update(const eagle4_conv_args* args, void* stream);
+
+/* ---- GDN tree recurrence, snapshot contract: kernels/gdn_tree_recurrence.py:204-359, 517-706 ----------------------- */
+typedef struct eagle4_gdn_args {
+  const void *q, *k, *v; /* q, k (1, tokens, H, K); v (1, tokens, HV, V); token-strided, unit inner strides */
+  int64_t stride_q, stride_k, stride_v;
+  int32_t in_dtype; /* q, k, v */
+  int32_t gate_dtype; /* a, b */
+  const void *a, *b; /* (tokens, HV) */
+  int64_t stride_a, stride_b;
+  const void *A_log, *dt_bias; /* [HV] */
+  int32_t A_log_dtype, dt_bias_dtype;
+  float softplus_beta, softplus_threshold, scale;
+  int32_t out_dtype;
+  void* out; /* (1, tokens, HV, V), contiguous over (HV, V) */
+  int64_t stride_o;
+  eagle4_itab parents;    /* [N, >= rows] parent row of each row */
+  eagle4_itab cu_seqlens; /* [N + 1] */
+  const void* h0_source;  /* [slots, HV, V, K] */
+  int64_t stride_h0_source;
+  int32_t h0_dtype;
+  int32_t snap_dtype;
+  eagle4_itab h0_indices;   /* [N] or [N, C] with num_accepted */
+  eagle4_itab num_accepted; /* [N] or null */
+  void* snap;               /* [slots, steps, HV, V, K] (per-request rows) or [slots, HV, V, K] (per-row slots) */
+  int64_t stride_snap_slot, stride_snap_row;
+  eagle4_itab snap_indices; /* [N] or [N, S] */
+  int32_t* publish;         /* [N, >= S] or null */
+  int64_t stride_publish;
+  int32_t num_slot_cols;
+  int32_t N, H, HV, K, V;
+  int32_t row_slots;
+  int32_t skip_chain_reload;
+  int32_t pad_slot_id;
+} eagle4_gdn_args;
+int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* args, void* stream);
+
+/* ---- GDN records contract: kernels/gdn_tree_records.py:16-101, 104-156, 160-272, 364-444 --------------------------- */
+typedef struct eagle4_records_args {
+  const void *q, *k, *v;
+  int64_t stride_q, stride_k, stride_v;
+  int32_t in_dtype, gate_dtype;
+  const void *a, *b;
+  int64_t stride_a, stride_b;
+  const void *A_log, *dt_bias;
+  int32_t A_log_dtype, dt_bias_dtype;
+  float scale;
+  int32_t out_dtype;
+  void* out; /* (1, tokens, HV, V) contiguous */
+  const void* state; /* pool [slots, HV, V, K] */
+  int64_t stride_state;
+  int32_t state_dtype;
+  int32_t round_state;
+  eagle4_itab state_indices;   /* [N] */
+  eagle4_itab query_start_loc; /* [N + 1] */
+  eagle4_itab parent;          /* [N, >= width] */
+  float* records;              /* [rows, steps, HV, REC] fp32 */
+  int64_t stride_records_row;
+  int32_t rec;
+  int32_t width;
+  eagle4_itab record_indices; /* [N] */
+  int32_t N, H, HV, K, V;
+  int32_t reserved;
+} eagle4_records_args;
+int eagle4_gdn_tree_records_update(const eagle4_records_args* args, void* stream);
+
+typedef struct eagle4_records_commit_args {
+  void* state; /* (L, slots, HV, V, K), contiguous (V, K) per head */
+  int64_t stride_state_layer, stride_state_slot;
+  int32_t state_dtype;
+  int32_t round_state;
+  const float* records; /* (L, rows, steps, HV, REC) */
+  int64_t stride_records_layer, stride_records_row;
+  eagle4_itab state_indices;  /* [n] */
+  eagle4_itab record_indices; /* [n] */
+  eagle4_itab commit_steps;   /* [n] */
+  eagle4_itab parent;         /* [n, width] */
+  int32_t n, layers, HV, K, V, rec, dmax;
+  int32_t reserved;
+} eagle4_records_commit_args;
+int eagle4_gdn_tree_records_commit(const eagle4_records_commit_args* args, void* stream);
+
+/* ---- tree-verify attention: vllm/verify_attention.py:29-207, kernels/online_softmax.py:11-24 ----------------------- */
+typedef struct eagle4_attn_args {
+  const void* q; /* [tokens, Hq, D] */
+  int64_t stride_qt, stride_qh;
+  const void* k_new; /* [tokens, Hkv, D] */
+  int64_t stride_knt, stride_knh;
+  const void* v_new;
+  int64_t stride_vnt, stride_vnh;
+  const void* key_cache; /* [blocks, page, Hkv, D] */
+  int64_t stride_kb, stride_ks, stride_kh;
+  const void* value_cache;
+  int64_t stride_vb, stride_vs, stride_vh;
+  const float* k_scale; /* [blocks, Hkv] fp32 (fp8 caches only) */
+  int64_t stride_ksb, stride_ksh;
+  const float* v_scale;
+  int64_t stride_vsb, stride_vsh;
+  eagle4_itab block_table;     /* [R, max_blocks] */
+  eagle4_itab context_lens;    /* [R] */
+  eagle4_itab query_start_loc; /* [R + 1] */
+  const int64_t* masks;        /* [R, >= max_query_len] */
+  int64_t stride_mask;
+  void* out; /* [tokens, Hq, D] */
+  int64_t stride_ot, stride_oh;
+  float* workspace; /* eagle4_verify_attention_workspace() bytes */
+  int64_t workspace_bytes;
+  float scale;
+  int32_t num_reqs, Hq, Hkv, D, page, max_query_len, max_blocks;
+  int32_t dtype;       /* q, k_new, v_new, out: EAGLE4_BF16 or EAGLE4_F16 */
+  int32_t cache_dtype; /* EAGLE4_BF16, EAGLE4_F16 or EAGLE4_FP8_E4M3 */
+  int32_t chunk;       /* context keys per split, a multiple of 64; 0: chosen from the sizes */
+} eagle4_attn_args;
+int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* args);
+int eagle4_verify_attention(const eagle4_attn_args* args, void* stream);
+
+/* ---- greedy accept: vllm/tree_accept.py:45-115 (walk), :195-216 (argmax of the greedy sampler) --------------------- */
+typedef struct eagle4_argmax_args {
+  const void* logits; /* [rows, vocab], unit column stride */
+  int64_t stride_row;
+  int32_t dtype;
+  int32_t rows;
+  int32_t vocab;
+  int32_t reserved;
+  int64_t* out; /* [rows] */
+} eagle4_argmax_args;
+int eagle4_argmax_rows(const eagle4_argmax_args* args, void* stream);
+
+typedef struct eagle4_accept_tree_args {
+  eagle4_itab target;        /* [num_logits] */
+  eagle4_itab drafted;       /* [num_logits] */
+  eagle4_itab cu_num_logits; /* [R + 1] */
+  eagle4_itab idx_mapping;   /* [R] */
+  eagle4_itab parents;       /* [slots, W] */
+  int64_t* sampled;          /* [R, >= W] */
+  int64_t stride_sampled;
+  int32_t* num_sampled; /* [R] */
+  int32_t* path;        /* [slots, >= W] */
+  int64_t stride_path;
+  int32_t* path_len; /* [slots] */
+  int32_t num_reqs, width;
+} eagle4_accept_tree_args;
+int eagle4_accept_tree(const eagle4_accept_tree_args* args, void* stream);
+
+/* ---- bs1 accept tail: kernels/accept_tail.py:56-224 ---------------------------------------------------------------- */
+typedef struct eagle4_accept_tail_args {
+  eagle4_itab target_predict, candidates, retrieve_index, retrieve_next_token, retrieve_next_sibling;
+  eagle4_itab seq_lens, out_cache_loc, req_to_token, req_pool_indices;
+  int32_t* predict;      /* [width] */
+  int32_t* accept_index; /* [depth] */
+  int32_t* accept_lens;  /* [1] */
+  void* new_seq_lens;    /* [1], seq_lens' dtype */
+  int32_t* bonus;        /* [1] */
+  int64_t* committed_slots; /* [depth] */
+  int64_t* accepted_slots;  /* [depth] */
+  int32_t width, depth;
+} eagle4_accept_tail_args;
+int eagle4_accept_tail(const eagle4_accept_tail_args* args, void* stream);
+
+typedef struct eagle4_compact_rows_args {
+  const void* src;
+  void* dst;
+  eagle4_itab accept_index; /* [1, depth] */
+  int64_t src_stride, dst_stride; /* bytes */
+  int64_t row_bytes;
+  int32_t width, depth;
+} eagle4_compact_rows_args;
+int eagle4_compact_rows(const eagle4_compact_rows_args* args, void* stream);
+
+/* ---- vLLM linear-state commit: vllm/gdn_tree_verify.py:186-322 ---------------------------------------------------- */
+typedef struct eagle4_state_commit_args {
+  const uint64_t* conv_ptrs;    /* [L] device array: each layer's window cache base */
+  const uint64_t* ssm_ptrs;     /* [L] device array: each layer's state pool base */
+  const uint64_t* slots_ptrs;   /* [L] device array: each layer group's [reqs, S] int32 slot table */
+  const int64_t* slots_strides; /* [L] device array */
+  eagle4_itab idx_mapping;      /* [R] */
+  eagle4_itab path;             /* [state slots, W] */
+  eagle4_itab path_len;         /* [state slots] */
+  int64_t conv_stride_slot, conv_stride_dim, conv_stride_tok; /* elements */
+  int64_t ssm_stride_slot;      /* elements */
+  int64_t ssm_numel;            /* elements per slot */
+  int32_t conv_dtype, ssm_dtype;
+  int32_t num_reqs, layers, dim;
+  int32_t reserved;
+} eagle4_state_commit_args;
+int eagle4_linear_state_commit(const eagle4_state_commit_args* args, void* stream);
+
+/* ---- library introspection ---------------------------------------------------------------------------------------- */
+const char* eagle4_version(void);
+/* sizeof() of argument struct `which` (0 stage, 1 ancestors, 2 tail words, 3 conv, 4 gdn, 5 records, 6 records commit,
+ * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit); -1 past the end. The host
+ * binding checks its struct mirrors against these. */
+int64_t eagle4_args_size(int which);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EAGLE4_AMD_H_ */

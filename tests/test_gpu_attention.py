@@ -1,0 +1,140 @@
+"""Tree-verify attention on the GPU against the dense oracle (vllm/verify_attention.py:142-207): bf16 / fp16 paged
+caches, GQA, ragged trees, single and multi-split contexts, fp8-e4m3 pages with per-(page, KV head) scales, and rows
+past the batch left untouched. Tolerance: 2e-2 absolute, 1e-2 relative (bf16 outputs)."""
+
+import pytest
+import torch
+
+from conftest import announce
+from oracle import attention as oa
+from oracle.tables import tree_masks
+from workloads import ATTN_B1, AttnShape, attention_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, inp, dtype, chunk=0, fp8=False):
+    from eagle_harness.vllm.verify_attention import verify_attention
+
+    g = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out = torch.full_like(g["q"], 7.0)
+    kw = dict(k_scale=g["k_scale"], v_scale=g["v_scale"]) if fp8 else {}
+    verify_attention(g["q"], g["k_new"], g["v_new"], g["key_cache"], g["value_cache"], g["block_table"],
+                     g["context_lens"], g["query_start_loc"], g["masks"], g["scale"], out,
+                     max_query_len=g["max_query_len"], chunk=chunk, **kw)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _want(inp, fp8=False):
+    out = torch.full_like(inp["q"], 7.0)
+    kw = dict(k_scale=inp["k_scale"], v_scale=inp["v_scale"]) if fp8 else {}
+    return oa.verify_attention(inp["q"], inp["k_new"], inp["v_new"], inp["key_cache"], inp["value_cache"],
+                               inp["block_table"], inp["context_lens"], inp["query_start_loc"], inp["masks"],
+                               inp["scale"], out, max_query_len=inp["max_query_len"], **kw)
+
+
+def _close(got, want):
+    torch.testing.assert_close(got.float(), want.float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize(
+    "contexts, parents, heads, kv_heads, d, page",
+    [
+        ([300], [[-1, 0, 0, 1, 1, 2, 3]], 6, 1, 64, 16),
+        ([5, 700, 0], [[-1, 0, 1], [-1, 0, 0, 1, 2, 2, 3, 4, 5], [-1, 0]], 4, 2, 32, 32),
+        ([129], [[-1] + [r - 1 for r in range(1, 24)]], 6, 1, 64, 16),
+        ([1500, 2], [[-1, 0, 0, 1], [-1, 0]], 8, 2, 128, 16),
+        ([1000], [[-1, 0, 1, 1, 3, 0]], 12, 2, 256, 48),  # a page size that is not a power of two
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, page, dtype):
+    """The reference test's cases (tests/test_verify_attention.py:31-92) plus wider heads and pages."""
+    announce(f"attention contexts={contexts} heads={heads}/{kv_heads} d={d} page={page} {dtype}")
+    gen = torch.Generator().manual_seed(len(contexts) * 100 + heads)
+    num_reqs = len(contexts)
+    widths = [len(p) for p in parents]
+    width = max(widths)
+    max_blocks = max(c // page + 1 for c in contexts) + 1
+    num_blocks = num_reqs * max_blocks + 3
+    kv = torch.randn(num_blocks, page, kv_heads, 2 * d, generator=gen).to(dtype)
+    key_cache, value_cache = kv[..., :d], kv[..., d:]
+    table = torch.randperm(num_blocks, generator=gen)[: num_reqs * max_blocks].view(num_reqs, max_blocks).int()
+    tokens = sum(widths)
+    inp = dict(
+        q=torch.randn(tokens + 2, heads, d, generator=gen).to(dtype),
+        k_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
+        v_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
+        key_cache=key_cache, value_cache=value_cache, block_table=table,
+        context_lens=torch.tensor(contexts, dtype=torch.int32),
+        query_start_loc=torch.tensor([0] + [sum(widths[: i + 1]) for i in range(num_reqs)], dtype=torch.int32),
+        masks=torch.tensor([tree_masks(p, width) for p in parents], dtype=torch.int64),
+        scale=d**-0.5, max_query_len=width,
+    )
+    want = _want(inp)
+    for chunk in (0, 64, 256):  # one split, many splits, the default
+        got = _run(dev, inp, dtype, chunk=chunk)
+        _close(got[:tokens], want[:tokens])
+        assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))  # rows past the batch untouched
+
+
+def test_b1_l512_workload(dev):
+    """Batch 1, 16 seeded nodes, prefix 512, 16 / 4 heads, D 128 (the oracle's fp32 CPU case, run in bf16)."""
+    announce("attention b1 l512")
+    inp = attention_inputs(ATTN_B1, seed=1, dtype=torch.bfloat16)
+    _close(_run(dev, inp, torch.bfloat16), _want(inp))
+
+
+@pytest.mark.parametrize("chunk", [0, 512])
+def test_b64_heads_short_batch(dev, chunk):
+    """The batch-64 workload's heads (24 / 4, D 256, page 16, permuted pages) at 6 requests with long prefixes."""
+    announce(f"attention d256 6 requests chunk={chunk}")
+    shape = AttnShape(6, 16, 24, 4, 256, 16, 1024, 4000)
+    inp = attention_inputs(shape, seed=4, dtype=torch.bfloat16)
+    _close(_run(dev, inp, torch.bfloat16, chunk=chunk), _want(inp))
+
+
+@pytest.mark.parametrize("chunk", [0, 256])
+def test_fp8_pages_match_dequantized_oracle(dev, chunk):
+    """fp8-e4m3 pages with per-(page, KV head) scales, dequantized in the tile loads; oracle: dequantize, then the
+    dense attention."""
+    announce(f"attention fp8 chunk={chunk}")
+    shape = AttnShape(4, 16, 24, 4, 256, 16, 300, 1800)
+    inp = attention_inputs(shape, seed=8, dtype=torch.bfloat16, fp8=True)
+    _close(_run(dev, inp, torch.bfloat16, chunk=chunk, fp8=True), _want(inp, fp8=True))
+
+
+def test_fp8_dequant_is_ocp_e4m3(dev):
+    """Every one of the 256 fp8 codes dequantizes as torch's float8_e4m3fn (OCP): one page whose keys and values
+    are the codes, attended by a single row with a one-hot query, reads them back exactly (bf16 outputs)."""
+    announce("attention fp8 code table")
+    d, page = 64, 16
+    codes = torch.arange(256, dtype=torch.uint8)
+    codes = codes[(codes & 0x7F) != 0x7F]  # NaN codes stay out
+    n = codes.numel()
+    keys = n // d + 1
+    pages = (keys + page - 1) // page
+    cache = torch.zeros(pages * page * d, dtype=torch.uint8)
+    cache[:n] = codes
+    cache = cache.view(torch.float8_e4m3fn).view(pages, page, 1, d)
+    value = cache.clone()
+    scale = torch.ones(pages, 1)
+    want_vals = value.float().view(pages * page, d)
+    # one row attends to exactly one context key through a dominant score: q along a key the others do not have
+    from eagle_harness.vllm.verify_attention import verify_attention
+
+    for kpos in range(keys):
+        kc = torch.zeros(pages * page, d)
+        kc[kpos, 0] = 448.0
+        key_cache = kc.to(torch.float8_e4m3fn).view(pages, page, 1, d)
+        q = torch.zeros(1, 1, d, dtype=torch.bfloat16)
+        q[0, 0, 0] = 1.0
+        out = torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev)
+        verify_attention(q.to(dev), torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev),
+                         torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev), key_cache.to(dev), value.to(dev),
+                         torch.arange(pages, dtype=torch.int32, device=dev)[None], torch.tensor([keys], dtype=torch.int32, device=dev),
+                         torch.tensor([0, 1], dtype=torch.int32, device=dev), torch.ones(1, 1, dtype=torch.int64, device=dev),
+                         1.0, out, max_query_len=1, k_scale=scale.to(dev), v_scale=scale.to(dev))
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out[0, 0].cpu().float(), want_vals[kpos].to(torch.bfloat16).float(), atol=0, rtol=0)
