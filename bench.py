@@ -1,0 +1,270 @@
+#!/usr/bin/env python
+"""Benchmark of the draft-tree verify hot path on one MI355X: verified tree tokens/s of one verify round.
+
+A step is one pass of the hot path over one batch of synthetic input, resident in HBM before the timed region:
+
+  1. verify stage (tree masks, depths, window codes, context lengths, depth positions);
+  2. tree-verify attention: batch 64, 16-node seeded trees, 24 query / 4 KV heads, D 256, bf16 paged KV (page 16,
+     permuted page tables), prefixes U[1024, 8192];
+  3. one GDN layer at the same batch: tree conv1d over the 8192 qkv channels, the gated delta rule walk with every
+     node's fp32 state snapshot (16 key / 32 value heads, K = V = 128), and the accepted-path commit (window
+     compaction, state move) for seeded accept lengths U[1, 12].
+
+``value`` = 64 x 16 verified tokens per step / step time. The JSON line also carries the dominant kernel's
+roofline (algorithmic HBM bytes per launch / its HIP-event duration, against MI355X's 8 TB/s) and the CPU baseline
+(the oracle, timed on a bounded sample on this host's cores). ``--calibrate-copy`` instead times a plain 1 GiB
+device copy (the reference kernel for the rocprofv3 FETCH_SIZE / WRITE_SIZE scale).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "eagle-4_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s (published)
+METRIC = "verified tree tokens/s (tree-attn+GDN) at B=64, T=16; % of HBM roofline"
+
+
+def _algorithmic_bytes(B, W, att, gdn, ctx, path_len, path_last):
+    """Bytes each kernel must move at least (every element once; re-reads and partials not counted)."""
+    import math
+
+    tokens = B * W
+    kv = sum(int(L) for L in ctx) * att["hkv"] * att["d"] * 2 * 2
+    pages = sum(math.ceil(int(L) / att["page"]) for L in ctx) * 4
+    attn = kv + pages + tokens * att["hq"] * att["d"] * 2 * 2 + tokens * att["hkv"] * att["d"] * 2 * 2 + B * W * 8
+    H, HV, K, V, dim = gdn["h"], gdn["hv"], gdn["k"], gdn["v"], gdn["dim"]
+    state = HV * K * V * 4
+    rec = B * state + tokens * state + tokens * H * K * 2 * 2 + tokens * HV * V * 2 + tokens * HV * 2 * 2
+    rec += tokens * HV * V * 2 + tokens * 4
+    conv = tokens * dim * 2 * 2 + B * dim * 3 * 2 + B * dim * (W + 2) * 2 + dim * 4 * 2
+    moved = sum(1 for n, last in zip(path_len, path_last) if last != n - 1)
+    commit = moved * 2 * state + sum(2 * max(n - 1, 0) for n in path_len) * dim * 2
+    stage = B * W * (4 + 12 + 8 + 8 + 8) + B * 4
+    return {"stage": stage, "attention": attn, "conv": conv, "recurrence": rec, "commit": commit}
+
+
+def _cpu_baseline(work, sample: int) -> dict:
+    """The oracle (torch on the host CPU) over the first ``sample`` requests of the workload."""
+    import torch
+
+    from oracle import attention as oa
+    from oracle import commit as ocm
+    from oracle import conv as oc
+    from oracle import recurrence as orr
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    W, B = work["W"], sample
+    a, g = work["attn_cpu"], work["gdn_cpu"]
+    t0 = time.perf_counter()
+    out = torch.empty_like(a["q"])
+    oa.verify_attention(a["q"], a["k_new"], a["v_new"], a["key_cache"], a["value_cache"], a["block_table"],
+                        a["context_lens"], a["query_start_loc"], a["masks"], a["scale"], out, max_query_len=W)
+    conv_out = torch.empty_like(g["x"])
+    oc.gdn_tree_conv1d_update(g["x"].t()[None], g["conv_state"], g["conv_weight"], None, "silu",
+                              g["slots"][:, 0].contiguous(), None, None, g["ancestors"], pad_slot_id=0,
+                              out=conv_out.t()[None], num_accepted_tokens=g["num_accepted"],
+                              query_start_loc=g["query_start_loc"])
+    HK = g["H"] * g["K"]
+    tokens = B * W
+    q = conv_out[:, :HK].reshape(1, tokens, g["H"], g["K"])
+    k = conv_out[:, HK : 2 * HK].reshape(1, tokens, g["H"], g["K"])
+    v = conv_out[:, 2 * HK :].reshape(1, tokens, g["HV"], g["V"])
+    orr.gdn_tree_recurrent_update(g["A_log"], g["dt_bias"], q, k, v, g["a"], g["b"], initial_state_source=g["pool"],
+                                  initial_state_indices=g["slots"], cu_seqlens=g["query_start_loc"],
+                                  intermediate_states_buffer=g["pool"], intermediate_state_indices=g["slots"],
+                                  retrieve_parent_token=g["parent_table"], num_accepted_tokens=g["num_accepted"],
+                                  pad_slot_id=0)
+    ocm.linear_state_commit([g["conv_state"]], [g["pool"]], [g["slots"]], torch.arange(B, dtype=torch.int32),
+                            g["path"], g["path_len"])
+    dt = time.perf_counter() - t0
+    return {"value": tokens / dt, "unit": "verified tree tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{sample} of 64 requests x 16 nodes through the CPU oracle (stage-free: attention, tree conv, "
+                      f"GDN walk with fp32 snapshots, commit), {dt:.2f} s on {threads} host threads"}
+
+
+def _calibrate_copy(steps: int) -> None:
+    import torch
+
+    dev = torch.device("cuda:0")
+    n = 1 << 30
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "ms": dt * 1e3,
+                      "GB/s (read+write)": 2 * n / dt / 1e9}), flush=True)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--chunk", type=int, default=0, help="attention context keys per split (0: the library's)")
+    ap.add_argument("--cpu-sample", type=int, default=4, help="requests in the CPU baseline's sample (0: skip)")
+    ap.add_argument("--calibrate-copy", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: the verify path needs no collective and this build runs on a single MI355X "
+              "(--gpus 1). Sharding is described in DESIGN.md.", file=sys.stderr)
+        return 2
+    import torch
+
+    if args.calibrate_copy:
+        _calibrate_copy(args.steps)
+        return 0
+
+    from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
+    from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+    from eagle_harness.vllm.gdn_tree_verify import LinearStateCommit
+    from eagle_harness.vllm.verify_attention import verify_attention
+    from eagle_harness.vllm.verify_layout import TreeStore, VerifyStage
+    from workloads import ATTN_B64, GDN_B64, accept_paths, attention_inputs, gdn_inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, W = ATTN_B64.batch, ATTN_B64.width
+    seed = 0
+    att = attention_inputs(ATTN_B64, seed=seed, device=dev, gen_device=dev)
+    gdn = gdn_inputs(GDN_B64, seed=seed, device=dev, layout="vllm", gen_device=dev)
+    parents = att["parents"]
+    assert parents == gdn["parents"]  # one tree per request drives both layers
+    tokens = B * W
+    store = TreeStore(B, W, dev)
+    store.parents.copy_(torch.tensor(parents, dtype=torch.int32))
+    stage = VerifyStage(B, tokens, W, dev)
+    chain_pos = (att["context_lens"].to(torch.int64)[:, None] + torch.arange(W, device=dev)).reshape(-1)
+    positions = chain_pos.clone()
+    idx = torch.arange(B, dtype=torch.int32, device=dev)
+    qsl = att["query_start_loc"]
+    path, path_len = accept_paths(parents, seed, W)
+    path_last = [int(path[b, int(path_len[b]) - 1]) for b in range(B)]
+    path_d, path_len_d = path.to(dev), path_len.to(dev)
+    commit = LinearStateCommit([(gdn["conv_state"], gdn["pool"])], [gdn["slots"]], dev)
+    out = torch.empty_like(att["q"])
+    conv_out = torch.empty_like(gdn["x"])
+    H, HV, K, V = GDN_B64.h, GDN_B64.hv, GDN_B64.k, GDN_B64.v
+    HK = H * K
+    q4 = conv_out[:, :HK].view(1, tokens, H, K)
+    k4 = conv_out[:, HK : 2 * HK].view(1, tokens, H, K)
+    v4 = conv_out[:, 2 * HK :].view(1, tokens, HV, V)
+    rec_out = torch.empty(1, tokens, HV, V, dtype=torch.bfloat16, device=dev)
+    slots0 = gdn["slots"][:, 0].contiguous()
+
+    # the CPU baseline's sample: the first requests, copied before any step mutates the states
+    work = None
+    if args.cpu_sample > 0:
+        S = args.cpu_sample
+        a_cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in att.items()}
+        a_cpu.update(q=a_cpu["q"][: S * W], k_new=a_cpu["k_new"][: S * W], v_new=a_cpu["v_new"][: S * W],
+                     block_table=a_cpu["block_table"][:S], context_lens=a_cpu["context_lens"][:S],
+                     query_start_loc=a_cpu["query_start_loc"][: S + 1], masks=a_cpu["masks"][:S])
+        nslot = 1 + S * (W + 1)
+        g_cpu = dict(x=gdn["x"][: S * W].cpu(), conv_state=gdn["conv_state"][:nslot].cpu(),
+                     conv_weight=gdn["conv_weight"].cpu(), slots=gdn["slots"][:S].cpu(),
+                     ancestors=gdn["ancestors"][:S].cpu(), num_accepted=gdn["num_accepted"][:S].cpu(),
+                     query_start_loc=gdn["query_start_loc"][: S + 1].cpu(), A_log=gdn["A_log"].cpu(),
+                     dt_bias=gdn["dt_bias"].cpu(), a=gdn["a"][: S * W].cpu(), b=gdn["b"][: S * W].cpu(),
+                     pool=gdn["pool"][:nslot].cpu(), parent_table=gdn["parent_table"][:S].cpu(), path=path[:S],
+                     path_len=path_len[:S], H=H, HV=HV, K=K, V=V)
+        work = dict(W=W, attn_cpu=a_cpu, gdn_cpu=g_cpu)
+
+    names = ["stage", "attention", "conv", "recurrence", "commit"]
+
+    def step(ev=None):
+        def mark(i):
+            if ev is not None:
+                ev[i].record()
+
+        mark(0)
+        stage.stage(store, idx, qsl, qsl, positions, B, tokens, tree=True)
+        mark(1)
+        verify_attention(att["q"], att["k_new"], att["v_new"], att["key_cache"], att["value_cache"],
+                         att["block_table"], stage.context_lens[:B], qsl, stage.masks[:B], att["scale"], out,
+                         max_query_len=W, chunk=args.chunk)
+        mark(2)
+        gdn_tree_conv1d_update(gdn["x"].t()[None], gdn["conv_state"], gdn["conv_weight"], None, "silu", slots0, None,
+                               None, stage.ancestors[:B], pad_slot_id=0, out=conv_out.t()[None],
+                               num_accepted_tokens=gdn["num_accepted"], query_start_loc=qsl)
+        mark(3)
+        gdn_tree_recurrent_update(gdn["A_log"], gdn["dt_bias"], q4, k4, v4, gdn["a"], gdn["b"],
+                                  initial_state_source=gdn["pool"], initial_state_indices=gdn["slots"],
+                                  cu_seqlens=qsl, intermediate_states_buffer=gdn["pool"],
+                                  intermediate_state_indices=gdn["slots"], retrieve_parent_token=stage.parents[:B],
+                                  num_accepted_tokens=gdn["num_accepted"], pad_slot_id=0, out=rec_out)
+        mark(4)
+        commit.commit(idx, path_d, path_len_d)
+        mark(5)
+        positions.copy_(chain_pos)  # the next round's chain positions (the stage rewrites them to depths)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = {n: sum(events[i][j].elapsed_time(events[i][j + 1]) for i in range(args.steps)) / args.steps
+           for j, n in enumerate(names)}
+    ctx = att["context_lens"].cpu().tolist()
+    nbytes = _algorithmic_bytes(B, W, dict(hq=ATTN_B64.hq, hkv=ATTN_B64.hkv, d=ATTN_B64.d, page=ATTN_B64.page),
+                                dict(h=H, hv=HV, k=K, v=V, dim=gdn["dim"]), ctx, path_len.tolist(), path_last)
+    kernels = {n: {"ms": per[n], "bytes": nbytes[n], "GB/s": nbytes[n] / (per[n] * 1e-3) / 1e9,
+                   "frac_of_hbm_peak": nbytes[n] / (per[n] * 1e-3) / HBM_PEAK} for n in names}
+    dominant = max(names, key=lambda n: per[n])
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dominant, {}).get("bytes_per_launch")
+    achieved = nbytes[dominant] / (per[dominant] * 1e-3)
+    step_bytes = sum(nbytes.values())
+    result = {
+        "metric": METRIC,
+        "value": tokens * args.steps / wall,
+        "unit": "verified tree tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded trees, prefixes, pages and tensors; random-init layer parameters)",
+        "config": {
+            "workload": "tree-verify attention (B64 T16, Hq24/Hkv4 D256 bf16, page 16, L~U[1024,8192]) + one GDN "
+                        "layer (tree conv1d + snapshot walk H16/HV32 K=V=128 fp32 states + accepted-path commit)",
+            "batch": B, "tree_nodes": W, "attention_chunk": args.chunk,
+            "step_hbm_bytes": step_bytes, "step_frac_of_hbm_roofline": step_bytes / (wall / args.steps) / HBM_PEAK,
+        },
+        "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic},
+        "kernels": kernels,
+        "cpu_baseline": _cpu_baseline(work, args.cpu_sample) if work is not None else None,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -2,22 +2,23 @@
 // rows (vllm/verify_attention.py:29-207, kernels/online_softmax.py:11-24).
 //
 // Roofline: HBM reads of the KV cache (~94 FLOP/B at batch 64, tree width 16, GQA 6, D 256; the bf16 MFMA ridge is
-// ~310 FLOP/B). The design reads every KV byte once:
+// ~310 FLOP/B). The design reads every KV byte once and keeps the reads in flight:
 //
-//  * One workgroup per (split of the context, KV head, request): its 4 waves own up to 4 tiles of 32 query rows,
-//    where a row is (draft token, query head of the KV head's group), so the G x W rows of a KV head share one read
-//    of each K / V tile (the reference's grid is per query head and re-reads every tile G times).
+//  * One workgroup per (split of the context, KV head, request). Its NW waves own 16 query rows each, where a row
+//    is (draft token, query head of the KV head's group), so all G x W rows of a KV head share one read of every
+//    K / V tile (the reference's grid is per query head and re-reads each tile G times).
 //  * Splits are fixed-size context chunks; a request uses ceil(L / chunk) of them (the grid is sized for the page
 //    table's capacity and idle splits exit at once). The last split also takes the draft keys, masked by the rows'
 //    ancestor bits. A request with one split writes its output directly; others write fp32 partials with their
 //    log2-sum-exp, merged by a second kernel.
-//  * 64-key tiles are staged in LDS: K row-major (row pitch D + 8 elements, conflict-free 16-byte reads), V transposed
-//    to [d][key] in registers (8x8 16-bit transposes) with an XOR swizzle so both the transposing writes and the
-//    MFMA operand reads are conflict-free. fp8 pages are dequantised (x * scale of the (page, KV head)) into the same
-//    16-bit tiles as they are staged.
-//  * Scores are S^T = K Q^T (v_mfma_f32_32x32x16): a lane then holds one query row's 16 scores per 32 keys, so the
-//    online softmax needs one cross-half exchange per row, and P^T is the B operand of O^T = V^T P^T directly in
-//    registers. O^T keeps one row per lane, so the rescale by exp2(m_old - m_new) is a per-lane multiply.
+//  * 32-key tiles are staged in LDS: K row-major (row pitch D + 8 elements: conflict-free 16-byte operand reads), V
+//    transposed to [d][key] in registers (8x8 16-bit transposes) under an XOR swizzle. A tile's K / V is loaded into
+//    registers one tile ahead and its page-table entries two tiles ahead, branch-free, so neither the page lookup
+//    nor the HBM read is exposed; fp8 pages are dequantised (x * scale of the (page, KV head)) at the LDS store.
+//  * Scores are S^T = K Q^T on v_mfma_f32_16x16x32: a lane then holds one query row's scores (4 lanes per row), so
+//    P^T is the B operand of O^T = V^T P^T straight from registers and O^T keeps one row per lane: the online
+//    softmax rescale is a per-lane multiply. 16 rows per wave keep O^T at D / 4 VGPRs per lane, leaving room for two
+//    workgroups per CU.
 
 #include <type_traits>
 
@@ -27,17 +28,17 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTileKeys = 64;
+constexpr int kTileKeys = 32;
 
 template <typename T>
-E4_DEV f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
+E4_DEV f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
   if constexpr (T::code == EAGLE4_BF16)
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
                                                   0, 0, 0);
 }
 
@@ -55,24 +56,6 @@ E4_DEV uint32_t pack2(float x, float y) {
   }
 }
 
-// 8x8 transpose of 16-bit values: in[i] holds d = 0..7 of key i; out[j] holds keys 0..7 of d = j.
-E4_DEV void transpose8x8(const uint4 (&in)[8], uint4 (&out)[8]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    uint32_t w[4];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint4& lo = in[2 * p];
-      const uint4& hi = in[2 * p + 1];
-      const uint32_t lw = (j >> 1) == 0 ? lo.x : (j >> 1) == 1 ? lo.y : (j >> 1) == 2 ? lo.z : lo.w;
-      const uint32_t hw = (j >> 1) == 0 ? hi.x : (j >> 1) == 1 ? hi.y : (j >> 1) == 2 ? hi.z : hi.w;
-      w[p] = __builtin_amdgcn_perm(hw, lw, sel);
-    }
-    out[j] = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-}
-
 // 8 fp8-e4m3 values (OCP) times a scale, rounded to 16-bit dtype T, packed.
 template <typename T>
 E4_DEV uint4 dequant8(uint2 raw, float scale) {
@@ -83,12 +66,6 @@ E4_DEV uint4 dequant8(uint2 raw, float scale) {
   auto pack = [scale](float x, float y) { return pack2<T>(x * scale, y * scale); };
   return make_uint4(pack(f0[0], f0[1]), pack(f1[0], f1[1]), pack(f2[0], f2[1]), pack(f3[0], f3[1]));
 }
-
-// The 8 keys of V-transpose group g (0..7) of a 64-key tile, in the order of the PV operand (key' = 8g + i).
-E4_DEV int group_key(int g, int i) { return 32 * (g >> 2) + 16 * ((g >> 1) & 1) + 8 * (i >> 2) + 4 * (g & 1) + (i & 3); }
-
-// Byte offset of the 16-byte chunk (row d, logical chunk g) of the swizzled V^T tile (rows of 64 keys = 128 bytes).
-E4_DEV int vt_offset(int d, int g) { return d * 128 + 16 * (g ^ ((d + (d >> 3)) & 7)); }
 
 struct Req {
   int64_t start, width, context;
@@ -132,120 +109,159 @@ E4_DEV void page_of(const KvAddr& k, int pos, int& blk_idx, int& slot) {
   }
 }
 
-// One thread's share of a 64-key K / V tile, loaded ahead into registers (raw cache bytes; fp8 with its scales) and
-// written to LDS one tile later, so the next tile's HBM reads overlap this tile's MFMAs.
-template <int D, bool FP8>
-struct TileRegs {
-  using Raw = typename std::conditional<FP8, uint2, uint4>::type;
-  static constexpr int NK = D / 32;  // K (key, 8-element chunk) pairs per thread: 64 * D / 8 / 256
-  Raw k[NK];
-  Raw v[8];
-  float ks[NK], vs[8];
+// ---- tile staging ---------------------------------------------------------------------------------------------------
+// A 32-key tile of K and of V lives in LDS row-major (rows of D 16-bit values) with its 16-byte chunks XOR-swizzled
+// per row, so both MFMA operand reads are conflict-free: K chunk c of key k sits at c ^ (k & 7); V chunk c at
+// c ^ 2 (k & 3). 16-bit pages are DMA'd straight into that layout with global_load_lds (lane p of an instruction
+// fills slot p; its source is the chunk the swizzle puts there); fp8 pages are loaded into registers and dequantised
+// into the same layout.
+
+template <int D>
+struct Tile {
+  static constexpr int CH = D / 8;           // 16-byte chunks per row
+  static constexpr int ROWB = 2 * D;         // bytes per row
+  static constexpr int BYTES = kTileKeys * ROWB;
+  static constexpr int RPI = 1024 / ROWB;    // rows one global_load_lds instruction fills (64 lanes x 16 bytes)
+  static constexpr int NI = kTileKeys / RPI;  // instructions per matrix per tile
+  static E4_DEV int kswz(int row) { return row & (CH < 8 ? CH - 1 : 7); }
+  static E4_DEV int vswz(int row) { return (2 * (row & 3)) & (CH - 1); }
 };
 
-template <int D, typename T, bool FP8>
-E4_DEV void load_tile(TileRegs<D, FP8>& r, const KvAddr& kv, int base, int hi, int tid) {
-  using Raw = typename TileRegs<D, FP8>::Raw;
-  constexpr int KCH = D / 8;
-  constexpr int EB = FP8 ? 1 : 2;  // bytes per element
-  const Raw zero{};
+// The pages of the rows a wave's direct loads fill (instructions n = wave + NW m), looked up two tiles ahead.
+template <int D, int NW>
+struct DirectPages {
+  static constexpr int NIW = (Tile<D>::NI + NW - 1) / NW;
+  int blk[NIW], slot[NIW];
+};
+
+template <int D, int NW>
+E4_DEV void lookup_direct(DirectPages<D, NW>& p, const KvAddr& kv, int base, int hi, int wave, int lane) {
+  using TL = Tile<D>;
 #pragma unroll
-  for (int i = 0; i < TileRegs<D, FP8>::NK; ++i) {
-    const int q = tid + 256 * i;
-    const int key = q / KCH, dc = q % KCH;
-    r.k[i] = zero;
-    r.ks[i] = 1.f;
-    const int pos = base + key;
-    if (pos < hi) {
-      int bi, sl;
-      page_of(kv, pos, bi, sl);
-      const int64_t blk = kv.bt[bi];
-      r.k[i] = *reinterpret_cast<const Raw*>(kv.kbase + blk * kv.kb + sl * kv.ks + 8 * EB * dc);
-      if constexpr (FP8) r.ks[i] = kv.kscale[blk * kv.ksb];
-    }
-  }
-  if (tid < 8 * KCH) {
-    const int g = tid / KCH, dc = tid % KCH;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      r.v[i] = zero;
-      r.vs[i] = 1.f;
-      const int pos = base + group_key(g, i);
-      if (pos < hi) {
-        int bi, sl;
-        page_of(kv, pos, bi, sl);
-        const int64_t blk = kv.bt[bi];
-        r.v[i] = *reinterpret_cast<const Raw*>(kv.vbase + blk * kv.vb + sl * kv.vs + 8 * EB * dc);
-        if constexpr (FP8) r.vs[i] = kv.vscale[blk * kv.vsb];
-      }
-    }
+  for (int m = 0; m < DirectPages<D, NW>::NIW; ++m) {
+    const int n = wave + NW * m;
+    const int pos = base + n * TL::RPI + lane / TL::CH;
+    int bi;
+    page_of(kv, pos < hi ? pos : hi - 1, bi, p.slot[m]);  // past the split: the split's last key (masked later)
+    p.blk[m] = n < TL::NI ? kv.bt[bi] : 0;
   }
 }
 
-// The draft keys / values (16-bit even with an fp8 cache) go straight into 16-bit registers.
-template <int D>
-E4_DEV void load_new_16(uint4 (&k)[D / 32], uint4 (&v)[8], const char* kn, const char* vn, int64_t skt, int64_t svt,
-                        int width, int tid) {
-  constexpr int KCH = D / 8;
+template <int D, int NW>
+E4_DEV void issue_direct_ctx(char* sKb, char* sVb, const DirectPages<D, NW>& p, const KvAddr& kv, int wave, int lane) {
+  using TL = Tile<D>;
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) {
-    const int q = tid + 256 * i;
-    const int key = q / KCH, dc = q % KCH;
-    k[i] = key < width ? *reinterpret_cast<const uint4*>(kn + key * skt + 16 * dc) : make_uint4(0, 0, 0, 0);
-  }
-  if (tid < 8 * KCH) {
-    const int g = tid / KCH, dc = tid % KCH;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int key = group_key(g, i);
-      v[i] = key < width ? *reinterpret_cast<const uint4*>(vn + key * svt + 16 * dc) : make_uint4(0, 0, 0, 0);
+  for (int m = 0; m < DirectPages<D, NW>::NIW; ++m) {
+    const int n = wave + NW * m;
+    if (n < TL::NI) {
+      const int row = n * TL::RPI + lane / TL::CH, pc = lane % TL::CH;
+      const int64_t off = static_cast<int64_t>(p.blk[m]) * kv.kb + static_cast<int64_t>(p.slot[m]) * kv.ks;
+      const int64_t offv = static_cast<int64_t>(p.blk[m]) * kv.vb + static_cast<int64_t>(p.slot[m]) * kv.vs;
+      // the builtin takes its source as a plain pointer variable (a compound expression fails its overload check)
+      const char* ksrc = kv.kbase + off + 16 * (pc ^ TL::kswz(row));
+      const char* vsrc = kv.vbase + offv + 16 * (pc ^ TL::vswz(row));
+      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 0);
     }
   }
 }
 
-template <int D>
-E4_DEV void store_tile_16(uint16_t* sK, uint16_t* sVt, const uint4 (&k)[D / 32], const uint4 (&v)[8], int tid) {
-  constexpr int KCH = D / 8, KP = D + 8;
+// Draft rows (16-bit): row r of the tile is draft key first + r, clamped to the last draft key (masked later).
+template <int D, int NW>
+E4_DEV void issue_direct_new(char* sKb, char* sVb, const char* knew, const char* vnew, int64_t kstride,
+                             int64_t vstride, int first, int width, int wave, int lane) {
+  using TL = Tile<D>;
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) {
-    const int q = tid + 256 * i;
-    *reinterpret_cast<uint4*>(&sK[(q / KCH) * KP + 8 * (q % KCH)]) = k[i];
-  }
-  if (tid < 8 * KCH) {
-    const int g = tid / KCH, dc = tid % KCH;
-    uint4 out[8];
-    transpose8x8(v, out);
-    char* vt = reinterpret_cast<char*>(sVt);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4*>(vt + vt_offset(8 * dc + j, g)) = out[j];
+  for (int m = 0; m < DirectPages<D, NW>::NIW; ++m) {
+    const int n = wave + NW * m;
+    if (n < TL::NI) {
+      const int row = n * TL::RPI + lane / TL::CH, pc = lane % TL::CH;
+      const int key = first + row < width ? first + row : width - 1;
+      const char* ksrc = knew + static_cast<int64_t>(key) * kstride + 16 * (pc ^ TL::kswz(row));
+      const char* vsrc = vnew + static_cast<int64_t>(key) * vstride + 16 * (pc ^ TL::vswz(row));
+      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 0);
+    }
   }
 }
 
-template <int D, typename T, bool FP8>
-E4_DEV void store_tile(uint16_t* sK, uint16_t* sVt, const TileRegs<D, FP8>& r, int tid) {
-  if constexpr (FP8) {
-    uint4 k[D / 32], v[8];
+// fp8 context tiles: (row, chunk) pairs q = tid + NT i, loaded raw into registers, dequantised into LDS later.
+template <int D, int NW>
+struct Fp8Tile {
+  static constexpr int NT = 64 * NW;
+  static constexpr int NQ = (kTileKeys * Tile<D>::CH + NT - 1) / NT;
+  uint2 k[NQ], v[NQ];
+  float ks[NQ], vs[NQ];
+};
+
+template <int D, int NW>
+E4_DEV void load_fp8(Fp8Tile<D, NW>& r, const KvAddr& kv, int base, int hi, int tid) {
+  using TL = Tile<D>;
+  constexpr int NT = 64 * NW;
+  int blk[Fp8Tile<D, NW>::NQ], sl[Fp8Tile<D, NW>::NQ];
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) k[i] = dequant8<T>(r.k[i], r.ks[i]);
+  for (int i = 0; i < Fp8Tile<D, NW>::NQ; ++i) {
+    const int q = tid + NT * i;
+    const int pos = base + q / TL::CH;
+    int bi;
+    page_of(kv, pos < hi ? pos : hi - 1, bi, sl[i]);
+    blk[i] = q < kTileKeys * TL::CH ? kv.bt[bi] : 0;
+  }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = dequant8<T>(r.v[i], r.vs[i]);
-    store_tile_16<D>(sK, sVt, k, v, tid);
+  for (int i = 0; i < Fp8Tile<D, NW>::NQ; ++i) {
+    const int q = tid + NT * i;
+    const int lc = q % TL::CH;
+    if (q < kTileKeys * TL::CH) {
+      const int64_t b = blk[i];
+      r.k[i] = *reinterpret_cast<const uint2*>(kv.kbase + b * kv.kb + static_cast<int64_t>(sl[i]) * kv.ks + 8 * lc);
+      r.v[i] = *reinterpret_cast<const uint2*>(kv.vbase + b * kv.vb + static_cast<int64_t>(sl[i]) * kv.vs + 8 * lc);
+      r.ks[i] = kv.kscale[b * kv.ksb];
+      r.vs[i] = kv.vscale[b * kv.vsb];
+    }
+  }
+}
+
+template <int D, int NW, typename T>
+E4_DEV void store_fp8(char* sKb, char* sVb, const Fp8Tile<D, NW>& r, int tid) {
+  using TL = Tile<D>;
+  constexpr int NT = 64 * NW;
+#pragma unroll
+  for (int i = 0; i < Fp8Tile<D, NW>::NQ; ++i) {
+    const int q = tid + NT * i;
+    if (q < kTileKeys * TL::CH) {
+      const int row = q / TL::CH, lc = q % TL::CH;
+      *reinterpret_cast<uint4*>(sKb + row * TL::ROWB + 16 * (lc ^ TL::kswz(row))) = dequant8<T>(r.k[i], r.ks[i]);
+      *reinterpret_cast<uint4*>(sVb + row * TL::ROWB + 16 * (lc ^ TL::vswz(row))) = dequant8<T>(r.v[i], r.vs[i]);
+    }
+  }
+}
+
+E4_DEV void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Starts tile `tile`'s K / V towards LDS buffer tile & 1: draft rows and 16-bit pages by direct loads, fp8 pages into
+// registers (dequantised and stored after this tile's compute).
+template <int D, int NW, typename T, bool FP8>
+E4_DEV void issue_tile(int tile, char (*smem)[2][Tile<D>::BYTES], int n_ctx, Fp8Tile<D, NW>& f8,
+                       const DirectPages<D, NW>& pages, const KvAddr& kv, int lo, int hi, const char* knp,
+                       const char* vnp, int64_t skt, int64_t svt, int width, int tid, int wave, int lane) {
+  char* kb = smem[tile & 1][0];
+  char* vb = smem[tile & 1][1];
+  if (tile >= n_ctx) {
+    issue_direct_new<D, NW>(kb, vb, knp, vnp, skt, svt, (tile - n_ctx) * kTileKeys, width, wave, lane);
+  } else if constexpr (FP8) {
+    load_fp8<D, NW>(f8, kv, lo + tile * kTileKeys, hi, tid);
   } else {
-    store_tile_16<D>(sK, sVt, r.k, r.v, tid);
+    issue_direct_ctx<D, NW>(kb, vb, pages, kv, wave, lane);
   }
 }
 
-template <int D, typename T, bool FP8>
-__global__ __launch_bounds__(256, 1) void verify_attention_kernel(const eagle4_attn_args a, int chunk, int row_tiles,
+template <int D, int NW, typename T, bool FP8>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void verify_attention_kernel(const eagle4_attn_args a, int chunk, int row_tiles,
                                                                   int max_splits) {
   static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
-  constexpr int KP = D + 8;  // K tile row pitch (elements)
-  // D = 256: the Q operands of the 4 waves live in LDS (rows of D + 8 elements) to leave registers to O^T and the
-  // prefetched tile; smaller heads keep them in registers.
-  constexpr bool kQInLds = D == 256;
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kTileKeys * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * kTileKeys];
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[kQInLds ? 4 * 32 * KP : 8];
+  using TL = Tile<D>;
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buffer][K, V]
 
   const int split = blockIdx.x;
   const int G = a.Hq / a.Hkv;
@@ -256,43 +272,36 @@ __global__ __launch_bounds__(256, 1) void verify_attention_kernel(const eagle4_a
   if (split >= rq.splits || rq.width <= 0) return;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int h = lane >> 5, l32 = lane & 31;
-  const int rt = rgroup * 4 + wave;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int rt = rgroup * NW + wave;
   const bool computes = rt < row_tiles;
-  const int rho = rt * 32 + l32;  // this lane's query row
+  const int rho = rt * 16 + l16;  // this lane's query row
   const int t = rho / G, gq = rho % G;
   const bool row_ok = computes && t < rq.width && t < a.max_query_len;
   const int64_t head = static_cast<int64_t>(kvh) * G + gq;
 
-  // Q of the lane's row: d = 16 s + 8 h + (0..7) for s < D / 16
-  constexpr int QN = kQInLds ? 1 : D / 16;
-  uint4 qreg[QN];
-  const uint16_t* sQrow = &sQ[kQInLds ? (wave * 32 + l32) * KP + 8 * h : 0];
+  // Q of the lane's row: d = 32 c + 8 g + (0..7) for c < D / 32 (the B operand of S^T = K Q^T)
+  uint4 qreg[D / 32];
   {
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (rq.start + t) * a.stride_qt + head * a.stride_qh + 8 * h;
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (rq.start + t) * a.stride_qt + head * a.stride_qh + 8 * g;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) {
-      const uint4 qv = row_ok ? *reinterpret_cast<const uint4*>(qp + 16 * s) : make_uint4(0, 0, 0, 0);
-      if constexpr (kQInLds)
-        *reinterpret_cast<uint4*>(const_cast<uint16_t*>(sQrow) + 16 * s) = qv;
-      else
-        qreg[s] = qv;
-    }
+    for (int c = 0; c < D / 32; ++c)
+      qreg[c] = row_ok ? *reinterpret_cast<const uint4*>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
   }
-  int64_t row_mask = 0;
-  if (row_ok) row_mask = a.masks[b * a.stride_mask + t];
+  const int64_t row_mask = row_ok ? a.masks[b * a.stride_mask + t] : 0;
 
-  f32x16_t acc[D / 32];
+  f32x4_t acc[D / 16];  // O^T: acc[dt][i] is d = 16 dt + 4 g + i of the lane's row
 #pragma unroll
-  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16_t{};
+  for (int i = 0; i < D / 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   const float scale_log2 = a.scale * 1.4426950408889634f;
 
-  const int64_t lo = static_cast<int64_t>(split) * chunk;  // context positions stay below 2^31
-  const int64_t hi = lo + chunk < rq.context ? lo + chunk : rq.context;
+  const int lo = split * chunk;  // context positions stay below 2^31
+  const int hi = static_cast<int>(lo + chunk < rq.context ? lo + chunk : rq.context);
   const bool has_new = split == rq.splits - 1;
-  const int n_ctx_tiles = hi > lo ? static_cast<int>((hi - lo + kTileKeys - 1) / kTileKeys) : 0;
-  const int n_tiles = n_ctx_tiles + (has_new ? 1 : 0);
+  const int width = static_cast<int>(rq.width < 64 ? rq.width : 64);
+  const int n_ctx = hi > lo ? (hi - lo + kTileKeys - 1) / kTileKeys : 0;
+  const int n_tiles = n_ctx + (has_new ? (width + kTileKeys - 1) / kTileKeys : 0);
 
   KvAddr kv;
   {
@@ -311,125 +320,125 @@ __global__ __launch_bounds__(256, 1) void verify_attention_kernel(const eagle4_a
     kv.page = a.page;
     kv.page_shift = (a.page & (a.page - 1)) == 0 ? __builtin_ctz(a.page) : -1;
   }
-  const int ilo = static_cast<int>(lo), ihi = static_cast<int>(hi);
-  TileRegs<D, FP8> pre;
-  if (n_ctx_tiles > 0) load_tile<D, T, FP8>(pre, kv, ilo, ihi, tid);
+  const char* knp = static_cast<const char*>(a.k_new) + (rq.start * a.stride_knt + kvh * a.stride_knh) * 2;
+  const char* vnp = static_cast<const char*>(a.v_new) + (rq.start * a.stride_vnt + kvh * a.stride_vnh) * 2;
+  const int64_t skt = a.stride_knt * 2, svt = a.stride_vnt * 2;
+
+  // pipeline: pages two tiles ahead, K / V one tile ahead (LDS double buffer); one barrier per tile
+  DirectPages<D, NW> pages;
+  Fp8Tile<D, NW> f8;
+  if constexpr (!FP8) {
+    if (n_ctx > 0) lookup_direct<D, NW>(pages, kv, lo, hi, wave, lane);
+  }
+  issue_tile<D, NW, T, FP8>(0, smem, n_ctx, f8, pages, kv, lo, hi, knp, vnp, skt, svt, width, tid, wave, lane);
+  if constexpr (FP8) {
+    if (n_ctx > 0) store_fp8<D, NW, T>(smem[0][0], smem[0][1], f8, tid);
+  } else {
+    if (n_ctx > 1) lookup_direct<D, NW>(pages, kv, lo + kTileKeys, hi, wave, lane);
+  }
+
   for (int tile = 0; tile < n_tiles; ++tile) {
-    const bool is_new = tile == n_ctx_tiles;
-    const int64_t base = lo + static_cast<int64_t>(tile) * kTileKeys;
-    // ---- stage this tile: K row-major, V transposed (the previous tile's MFMAs are done: barrier) -------------------
-    __syncthreads();
-    if (is_new) {
-      uint4 kn[D / 32], vn[8];
-      const char* knp = static_cast<const char*>(a.k_new) + (rq.start * a.stride_knt + kvh * a.stride_knh) * 2;
-      const char* vnp = static_cast<const char*>(a.v_new) + (rq.start * a.stride_vnt + kvh * a.stride_vnh) * 2;
-      load_new_16<D>(kn, vn, knp, vnp, a.stride_knt * 2, a.stride_vnt * 2, static_cast<int>(rq.width), tid);
-      store_tile_16<D>(sK, sVt, kn, vn, tid);
-    } else {
-      store_tile<D, T, FP8>(sK, sVt, pre, tid);
+    const bool is_new = tile >= n_ctx;
+    const int base = is_new ? (tile - n_ctx) * kTileKeys : lo + tile * kTileKeys;  // new tiles: draft row index
+    wait_vmem();  // this tile's DMA (issued a tile ago) has landed; the page lookups too
+    __syncthreads();  // ... for every wave, and the other buffer is no longer read
+    if (tile + 1 < n_tiles) {
+      issue_tile<D, NW, T, FP8>(tile + 1, smem, n_ctx, f8, pages, kv, lo, hi, knp, vnp, skt, svt, width, tid, wave,
+                                lane);
+      if constexpr (!FP8) {
+        if (tile + 2 < n_ctx) lookup_direct<D, NW>(pages, kv, lo + (tile + 2) * kTileKeys, hi, wave, lane);
+      }
     }
-    __syncthreads();
-    if (tile + 1 < n_ctx_tiles) load_tile<D, T, FP8>(pre, kv, static_cast<int>(base) + kTileKeys, ihi, tid);
+    const char* sKb = smem[tile & 1][0];
+    const char* sVb = smem[tile & 1][1];
 
     if (computes) {
-      // ---- S^T = K Q^T for keys 0..31 and 32..63 ----------------------------------------------------------------
-      f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+      // ---- S^T = K Q^T for keys 0..15 and 16..31: s[kt][i] is key 16 kt + 4 g + i of the lane's row ----------
+      f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        const uint16_t* kr = &sK[(32 * sb + l32) * KP + 8 * h];
+      for (int kt = 0; kt < 2; ++kt) {
+        const int key = 16 * kt + l16;
+        const char* kr = sKb + key * TL::ROWB;
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-          uint4 qv;
-          if constexpr (kQInLds)
-            qv = *reinterpret_cast<const uint4*>(sQrow + 16 * c);
-          else
-            qv = qreg[c];
-          s[sb] = mfma32<T>(*reinterpret_cast<const uint4*>(kr + 16 * c), qv, s[sb]);
-          // keep the operand reads next to their MFMAs (hoisting them all costs a register per byte of the tile)
-          if ((c & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int c = 0; c < D / 32; ++c)
+          s[kt] = mfma16<T>(*reinterpret_cast<const uint4*>(kr + 16 * ((4 * c + g) ^ TL::kswz(key))), qreg[c], s[kt]);
       }
-      // ---- mask, online softmax (log2 domain) -------------------------------------------------------------------
+      // ---- mask, online softmax (log2 domain; 4 lanes share a row) ----------------------------------------------
       float tmax = -INFINITY;
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int key = 32 * sb + 8 * (j >> 2) + 4 * h + (j & 3);
-          bool ok;
-          if (is_new)
-            ok = key < rq.width && ((row_mask >> key) & 1);
-          else
-            ok = static_cast<int>(base) + key < ihi;
-          const float v = ok ? s[sb][j] * scale_log2 : -INFINITY;
-          s[sb][j] = v;
+        for (int i = 0; i < 4; ++i) {
+          const int key = base + 16 * kt + 4 * g + i;
+          const bool ok = is_new ? (key < width && ((row_mask >> key) & 1)) : key < hi;
+          const float v = ok ? s[kt][i] * scale_log2 : -INFINITY;
+          s[kt][i] = v;
           tmax = fmaxf(tmax, v);
         }
       }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
       const float m_new = fmaxf(m, tmax);
       const float safe = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = exp2f(m - safe);
       float psum = 0.f;
-      uint4 pb[4];
+      uint32_t w[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        uint32_t w[4];
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float p0 = exp2f(s[c >> 1][8 * (c & 1) + 2 * p] - safe);
-          const float p1 = exp2f(s[c >> 1][8 * (c & 1) + 2 * p + 1] - safe);
-          psum += p0 + p1;
-          w[p] = pack2<T>(p0, p1);
-        }
-        pb[c] = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int p = 0; p < 4; ++p) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4
+        const float p0 = exp2f(s[p >> 1][2 * (p & 1)] - safe);
+        const float p1 = exp2f(s[p >> 1][2 * (p & 1) + 1] - safe);
+        psum += p0 + p1;
+        w[p] = pack2<T>(p0, p1);
       }
+      const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+      psum += __shfl_xor(psum, 16, 64);
       psum += __shfl_xor(psum, 32, 64);
       l = l * alpha + psum;
       m = m_new;
-      // ---- O^T = O^T * alpha + V^T P^T -------------------------------------------------------------------------
-      const char* vt = reinterpret_cast<const char*>(sVt);
+      // ---- O^T = O^T * alpha + V^T P^T: V^T operands by transposing LDS reads of the row-major tile ------------
+      const int j = l16 >> 2, s4 = l16 & 3;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) {
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const int lc = 2 * dt + (s4 >> 1), half = 8 * (s4 & 1);
+        const int k0 = 4 * g + j, k1 = 16 + 4 * g + j;
+        const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(sVb + k0 * TL::ROWB + 16 * (lc ^ TL::vswz(k0)) + half));
+        const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4i16*)(sVb + k1 * TL::ROWB + 16 * (lc ^ TL::vswz(k1)) + half));
+        uint4 va;
+        va.x = __builtin_bit_cast(uint2, lo4).x;
+        va.y = __builtin_bit_cast(uint2, lo4).y;
+        va.z = __builtin_bit_cast(uint2, hi4).x;
+        va.w = __builtin_bit_cast(uint2, hi4).y;
         acc[dt] *= alpha;
-        const int d = 32 * dt + l32;
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          acc[dt] = mfma32<T>(*reinterpret_cast<const uint4*>(vt + vt_offset(d, 2 * c + h)), pb[c], acc[dt]);
-        __builtin_amdgcn_sched_barrier(0);
+        acc[dt] = mfma16<T>(va, pb, acc[dt]);
       }
+    }
+    if constexpr (FP8) {  // the next context tile's dequantised K / V into the other buffer (read after the barrier)
+      if (tile + 1 < n_ctx) store_fp8<D, NW, T>(smem[(tile + 1) & 1][0], smem[(tile + 1) & 1][1], f8, tid);
     }
   }
 
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   if (rq.splits == 1) {
-    uint16_t* op = static_cast<uint16_t*>(a.out) + (rq.start + t) * a.stride_ot + head * a.stride_oh;
+    uint16_t* op = static_cast<uint16_t*>(a.out) + (rq.start + t) * a.stride_ot + head * a.stride_oh + 4 * g;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = 32 * dt + 8 * g4 + 4 * h;
-        uint2 w;
-        w.x = static_cast<uint32_t>(T::from_f32(acc[dt][4 * g4] * inv)) |
-              (static_cast<uint32_t>(T::from_f32(acc[dt][4 * g4 + 1] * inv)) << 16);
-        w.y = static_cast<uint32_t>(T::from_f32(acc[dt][4 * g4 + 2] * inv)) |
-              (static_cast<uint32_t>(T::from_f32(acc[dt][4 * g4 + 3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(op + d) = w;
-      }
+    for (int dt = 0; dt < D / 16; ++dt) {
+      uint2 w;
+      w.x = pack2<T>(acc[dt][0] * inv, acc[dt][1] * inv);
+      w.y = pack2<T>(acc[dt][2] * inv, acc[dt][3] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * dt) = w;
+    }
   } else {
-    const int rows = row_tiles * 32;
+    const int rows = row_tiles * 16;
     const int64_t part = ((static_cast<int64_t>(b) * a.Hkv + kvh) * max_splits + split) * rows + rho;
-    float* pp = a.workspace + part * D;
+    float* pp = a.workspace + part * D + 4 * g;
 #pragma unroll
-    for (int dt = 0; dt < D / 32; ++dt)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = 32 * dt + 8 * g4 + 4 * h;
-        *reinterpret_cast<float4*>(pp + d) = make_float4(acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv,
-                                                         acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv);
-      }
-    if (h == 0) {
+    for (int dt = 0; dt < D / 16; ++dt)
+      *reinterpret_cast<float4*>(pp + 16 * dt) =
+          make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+    if (g == 0) {
       float* lse = a.workspace + static_cast<int64_t>(a.num_reqs) * a.Hkv * max_splits * rows * D;
       lse[part] = l > 0.f ? m + log2f(l) : -INFINITY;
     }
@@ -449,7 +458,7 @@ __global__ __launch_bounds__(256) void verify_merge_kernel(const eagle4_attn_arg
   const int d = 4 * (threadIdx.x % TPR);
   const int G = a.Hq / a.Hkv;
   const int t = rho / G, gq = rho % G;
-  const int rows = row_tiles * 32;
+  const int rows = row_tiles * 16;
   if (rho >= rows || t >= rq.width) return;
   const float* lse = a.workspace + static_cast<int64_t>(a.num_reqs) * a.Hkv * max_splits * rows * D;
   const int64_t part0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * max_splits * rows + rho;
@@ -477,15 +486,18 @@ __global__ __launch_bounds__(256) void verify_merge_kernel(const eagle4_attn_arg
 }
 
 struct Plan {
-  int chunk, row_tiles, row_groups, max_splits;
+  int chunk, row_tiles, waves, row_groups, max_splits;
 };
 
+// 16-row tiles; a workgroup takes up to 8 of them (more rows: more row groups, each reading the KV once).
 Plan plan(const eagle4_attn_args& a) {
   Plan p;
   p.chunk = a.chunk > 0 ? a.chunk : 1024;
   const int G = a.Hq / a.Hkv;
-  p.row_tiles = e4::ceil_div(static_cast<int64_t>(G) * a.max_query_len, 32);
-  p.row_groups = e4::ceil_div(p.row_tiles, 4);
+  p.row_tiles = e4::ceil_div(static_cast<int64_t>(G) * a.max_query_len, 16);
+  const int need = p.row_tiles < 8 ? p.row_tiles : 8;
+  p.waves = need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 6 ? 6 : 8));
+  p.row_groups = e4::ceil_div(p.row_tiles, p.waves);
   const int64_t capacity = static_cast<int64_t>(a.max_blocks) * a.page;
   p.max_splits = capacity > 0 ? e4::ceil_div(capacity, p.chunk) : 1;
   return p;
@@ -500,6 +512,7 @@ bool covered(const eagle4_attn_args& a) {
   if (a.cache_dtype == EAGLE4_FP8_E4M3 && (a.k_scale == nullptr || a.v_scale == nullptr)) return false;
   const int chunk = a.chunk > 0 ? a.chunk : 1024;
   if (chunk % kTileKeys != 0) return false;
+  if (static_cast<int64_t>(a.max_blocks) * a.page >= (int64_t(1) << 31)) return false;  // 32-bit positions
   // 16-byte vector accesses along D
   if ((a.stride_qt | a.stride_qh | a.stride_knt | a.stride_knh | a.stride_vnt | a.stride_vnh | a.stride_ot |
        a.stride_oh) % 8 != 0)
@@ -513,23 +526,33 @@ bool covered(const eagle4_attn_args& a) {
   return true;
 }
 
-template <int D, typename T, bool FP8>
+template <int D, int NW, typename T, bool FP8>
 int launch(const eagle4_attn_args& a, const Plan& p, hipStream_t s) {
   const dim3 grid(p.max_splits, a.Hkv * p.row_groups, a.num_reqs);
-  verify_attention_kernel<D, T, FP8><<<grid, 256, 0, s>>>(a, p.chunk, p.row_tiles, p.max_splits);
+  verify_attention_kernel<D, NW, T, FP8><<<grid, 64 * NW, 0, s>>>(a, p.chunk, p.row_tiles, p.max_splits);
   if (p.max_splits > 1) {
     constexpr int RPB = 256 / (D / 4);
-    const dim3 mgrid(e4::ceil_div(p.row_tiles * 32, RPB), a.Hkv, a.num_reqs);
+    const dim3 mgrid(e4::ceil_div(p.row_tiles * 16, RPB), a.Hkv, a.num_reqs);
     verify_merge_kernel<D, T><<<mgrid, 256, 0, s>>>(a, p.chunk, p.row_tiles, p.max_splits);
   }
   return E4_LAUNCH_STATUS();
 }
 
+template <int D, typename T, bool FP8>
+int launch_w(const eagle4_attn_args& a, const Plan& p, hipStream_t s) {
+  switch (p.waves) {
+    case 2: return launch<D, 2, T, FP8>(a, p, s);
+    case 4: return launch<D, 4, T, FP8>(a, p, s);
+    case 6: return launch<D, 6, T, FP8>(a, p, s);
+    default: return launch<D, 8, T, FP8>(a, p, s);
+  }
+}
+
 template <int D>
 int launch_d(const eagle4_attn_args& a, const Plan& p, hipStream_t s) {
   const bool fp8 = a.cache_dtype == EAGLE4_FP8_E4M3;
-  if (a.dtype == EAGLE4_BF16) return fp8 ? launch<D, e4::Bf16, true>(a, p, s) : launch<D, e4::Bf16, false>(a, p, s);
-  return fp8 ? launch<D, e4::F16, true>(a, p, s) : launch<D, e4::F16, false>(a, p, s);
+  if (a.dtype == EAGLE4_BF16) return fp8 ? launch_w<D, e4::Bf16, true>(a, p, s) : launch_w<D, e4::Bf16, false>(a, p, s);
+  return fp8 ? launch_w<D, e4::F16, true>(a, p, s) : launch_w<D, e4::F16, false>(a, p, s);
 }
 
 }  // namespace
@@ -538,7 +561,7 @@ extern "C" int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* a) 
   if (!covered(*a)) return -1;
   const Plan p = plan(*a);
   if (p.max_splits <= 1) return 0;
-  const int64_t parts = static_cast<int64_t>(a->num_reqs) * a->Hkv * p.max_splits * p.row_tiles * 32;
+  const int64_t parts = static_cast<int64_t>(a->num_reqs) * a->Hkv * p.max_splits * p.row_tiles * 16;
   return parts * (a->D + 1) * static_cast<int64_t>(sizeof(float));
 }
 

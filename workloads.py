@@ -103,12 +103,12 @@ ATTN_B512_FP8 = AttnShape(512, 16, 24, 4, 256, 16, 512, 4096)
 
 
 def attention_inputs(shape: AttnShape, seed: int, device="cpu", dtype=torch.bfloat16, fp8: bool = False,
-                     scale_qkv: float = 0.5) -> dict:
+                     scale_qkv: float = 0.5, gen_device="cpu") -> dict:
     """Inputs of ``verify_attention`` for a workload: seeded trees, prefix lengths, a permuted page table over all
     pages plus one spare page (never read), Q/K/V ~ N(0,1) * ``scale_qkv`` (fp8 caches: N(0,1), quantized per
     (page, KV head) with amax / 448)."""
     rng = np.random.default_rng(seed)
-    gen = torch.Generator(device="cpu").manual_seed(seed)
+    gen = torch.Generator(device=gen_device).manual_seed(seed)
     B, W = shape.batch, shape.width
     parents = [seeded_tree(rng, W) for _ in range(B)]
     lens = rng.integers(shape.lmin, shape.lmax + 1, size=B)
@@ -122,12 +122,13 @@ def attention_inputs(shape: AttnShape, seed: int, device="cpu", dtype=torch.bflo
         table[b, :nb] = perm[off : off + nb]
         off += nb
     tokens = B * W
-    q = (torch.randn(tokens, shape.hq, shape.d, generator=gen) * scale_qkv).to(dtype)
-    k_new = (torch.randn(tokens, shape.hkv, shape.d, generator=gen) * scale_qkv).to(dtype)
-    v_new = (torch.randn(tokens, shape.hkv, shape.d, generator=gen) * scale_qkv).to(dtype)
+    rnd = lambda *sz: torch.randn(*sz, generator=gen, device=gen_device)  # noqa: E731
+    q = (rnd(tokens, shape.hq, shape.d) * scale_qkv).to(dtype)
+    k_new = (rnd(tokens, shape.hkv, shape.d) * scale_qkv).to(dtype)
+    v_new = (rnd(tokens, shape.hkv, shape.d) * scale_qkv).to(dtype)
     kscale = 1.0 if fp8 else scale_qkv
-    key_cache = torch.randn(num_blocks, shape.page, shape.hkv, shape.d, generator=gen) * kscale
-    value_cache = torch.randn(num_blocks, shape.page, shape.hkv, shape.d, generator=gen) * kscale
+    key_cache = rnd(num_blocks, shape.page, shape.hkv, shape.d) * kscale
+    value_cache = rnd(num_blocks, shape.page, shape.hkv, shape.d) * kscale
     out = dict(parents=parents, context_lens=torch.tensor(lens, dtype=torch.int32), block_table=table, q=q,
                k_new=k_new, v_new=v_new, query_start_loc=torch.arange(0, tokens + 1, W, dtype=torch.int32),
                masks=torch.tensor([tree_masks(p) for p in parents], dtype=torch.int64), scale=shape.d**-0.5,
@@ -166,7 +167,7 @@ GDN_B256 = GdnShape(256, 16, 16, 32, 128, 128)
 
 
 def gdn_inputs(shape: GdnShape, seed: int, device="cpu", layout: str = "vllm", state_dtype=torch.float32,
-               in_dtype=torch.bfloat16, history: int = 3) -> dict:
+               in_dtype=torch.bfloat16, history: int = 3, gen_device="cpu") -> dict:
     """A GDN layer's tree verify inputs.
 
     q/k ~ N(0,1) (the kernel L2-normalizes them), v ~ N(0,1), a and b ~ N(0,1) with A_log = dt_bias = 0 (so
@@ -178,20 +179,20 @@ def gdn_inputs(shape: GdnShape, seed: int, device="cpu", layout: str = "vllm", s
     [requests, steps, HV, V, K] snapshot scratch.
     """
     rng = np.random.default_rng(seed)
-    gen = torch.Generator(device="cpu").manual_seed(seed + 1)
+    gen = torch.Generator(device=gen_device).manual_seed(seed + 1)
     B, W, H, HV, K, V = shape.batch, shape.width, shape.h, shape.hv, shape.k, shape.v
     parents = [seeded_tree(rng, W) for _ in range(B)]
     tokens = B * W
     dim = 2 * H * K + HV * V
-    x = torch.randn(tokens, dim, generator=gen).to(in_dtype)  # the packed projection, token-major
-    conv_w = (torch.randn(dim, 4, generator=gen) * 0.3).to(in_dtype)
-    q = torch.randn(1, tokens, H, K, generator=gen).to(in_dtype)
-    k = torch.randn(1, tokens, H, K, generator=gen).to(in_dtype)
-    v = torch.randn(1, tokens, HV, V, generator=gen).to(in_dtype)
-    a = torch.randn(tokens, HV, generator=gen).to(in_dtype)
-    b = torch.randn(tokens, HV, generator=gen).to(in_dtype)
-    A_log = torch.zeros(HV)
-    dt_bias = torch.zeros(HV)
+    x = torch.randn(device=gen_device, size=(tokens, dim,), generator=gen).to(in_dtype)  # the packed projection, token-major
+    conv_w = (torch.randn(device=gen_device, size=(dim, 4,), generator=gen) * 0.3).to(in_dtype)
+    q = torch.randn(device=gen_device, size=(1, tokens, H, K,), generator=gen).to(in_dtype)
+    k = torch.randn(device=gen_device, size=(1, tokens, H, K,), generator=gen).to(in_dtype)
+    v = torch.randn(device=gen_device, size=(1, tokens, HV, V,), generator=gen).to(in_dtype)
+    a = torch.randn(device=gen_device, size=(tokens, HV,), generator=gen).to(in_dtype)
+    b = torch.randn(device=gen_device, size=(tokens, HV,), generator=gen).to(in_dtype)
+    A_log = torch.zeros(HV, device=gen_device)
+    dt_bias = torch.zeros(HV, device=gen_device)
     par = torch.tensor(parents, dtype=torch.int32)
     anc = torch.tensor([list(zip(*window_codes(p))) for p in parents], dtype=torch.int32)  # [B, 3, W]
     qsl = torch.arange(0, tokens + 1, W, dtype=torch.int32)
@@ -200,19 +201,19 @@ def gdn_inputs(shape: GdnShape, seed: int, device="cpu", layout: str = "vllm", s
     if layout == "vllm":
         # slots[b] = W + 1 per-row slots (row i -> slot 1 + b (W + 1) + i); slot 0 is the null block
         slots = (1 + torch.arange(B * (W + 1), dtype=torch.int32)).view(B, W + 1)
-        pool = torch.zeros(1 + B * (W + 1), HV, V, K, dtype=state_dtype)
-        init = torch.randn(B, HV, V, K, generator=gen) * 0.02
+        pool = torch.zeros(1 + B * (W + 1), HV, V, K, dtype=state_dtype, device=gen_device)
+        init = torch.randn(device=gen_device, size=(B, HV, V, K,), generator=gen) * 0.02
         pool[slots[:, 0].long()] = init.to(state_dtype)
-        conv_state = torch.zeros(1 + B * (W + 1), dim, history + W, dtype=in_dtype)
-        conv_state[slots[:, 0].long(), :, :3] = torch.randn(B, dim, 3, generator=gen).to(in_dtype)
+        conv_state = torch.zeros(1 + B * (W + 1), dim, history + W, dtype=in_dtype, device=gen_device)
+        conv_state[slots[:, 0].long(), :, :3] = torch.randn(device=gen_device, size=(B, dim, 3,), generator=gen).to(in_dtype)
         out.update(slots=slots, pool=pool, num_accepted=torch.ones(B, dtype=torch.int32), conv_state=conv_state)
     else:
-        pool = (torch.randn(B + 1, HV, V, K, generator=gen) * 0.02).to(state_dtype)
-        scratch = torch.zeros(B, W, HV, V, K, dtype=state_dtype)
-        conv_state = torch.randn(B + 1, dim, 3, generator=gen).to(in_dtype)
+        pool = (torch.randn(device=gen_device, size=(B + 1, HV, V, K,), generator=gen) * 0.02).to(state_dtype)
+        scratch = torch.zeros(B, W, HV, V, K, dtype=state_dtype, device=gen_device)
+        conv_state = torch.randn(device=gen_device, size=(B + 1, dim, 3,), generator=gen).to(in_dtype)
         out.update(pool=pool, state_indices=torch.arange(1, B + 1, dtype=torch.int32), scratch=scratch,
                    scratch_indices=torch.arange(B, dtype=torch.int32), conv_state=conv_state,
-                   windows=torch.zeros(B, W, dim, 3, dtype=in_dtype))
+                   windows=torch.zeros(B, W, dim, 3, dtype=in_dtype, device=gen_device))
     return {kk: (vv.to(device) if isinstance(vv, torch.Tensor) else vv) for kk, vv in out.items()}
 
 
