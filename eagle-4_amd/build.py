@@ -35,6 +35,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions. The streamed attention kernel keeps its MFMA accumulators in VGPRs (the default AGPR form makes
+# LLVM shuttle them between the two files every iteration at this register pressure).
+EXTRA_FLAGS = {"verify_attention_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if cand and Path(cand).exists():
@@ -44,7 +49,7 @@ def _hipcc() -> str:
 
 def _compile(hipcc: str, src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")

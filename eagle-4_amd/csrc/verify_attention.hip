@@ -22,50 +22,11 @@
 
 #include <type_traits>
 
-#include "common.h"
+#include "attention_tile.h"
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-constexpr int kTileKeys = 32;
-
-template <typename T>
-E4_DEV f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
-  if constexpr (T::code == EAGLE4_BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                  0, 0, 0);
-}
-
-// Two fp32 values rounded (nearest even) to 16-bit dtype T and packed, low first: one v_cvt_pk_* on gfx950.
-template <typename T>
-E4_DEV uint32_t pack2(float x, float y) {
-  if constexpr (T::code == EAGLE4_BF16) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    const bf16x2_t v = {static_cast<__bf16>(x), static_cast<__bf16>(y)};
-    return __builtin_bit_cast(uint32_t, v);
-  } else {
-    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-    const f16x2_t v = {static_cast<_Float16>(x), static_cast<_Float16>(y)};
-    return __builtin_bit_cast(uint32_t, v);
-  }
-}
-
-// 8 fp8-e4m3 values (OCP) times a scale, rounded to 16-bit dtype T, packed.
-template <typename T>
-E4_DEV uint4 dequant8(uint2 raw, float scale) {
-  const auto f0 = __builtin_amdgcn_cvt_pk_f32_fp8(raw.x, false);  // bytes 0, 1
-  const auto f1 = __builtin_amdgcn_cvt_pk_f32_fp8(raw.x, true);   // bytes 2, 3
-  const auto f2 = __builtin_amdgcn_cvt_pk_f32_fp8(raw.y, false);
-  const auto f3 = __builtin_amdgcn_cvt_pk_f32_fp8(raw.y, true);
-  auto pack = [scale](float x, float y) { return pack2<T>(x * scale, y * scale); };
-  return make_uint4(pack(f0[0], f0[1]), pack(f1[0], f1[1]), pack(f2[0], f2[1]), pack(f3[0], f3[1]));
-}
+using namespace e4attn;
 
 struct Req {
   int64_t start, width, context;
@@ -108,24 +69,6 @@ E4_DEV void page_of(const KvAddr& k, int pos, int& blk_idx, int& slot) {
     slot = pos - blk_idx * k.page;
   }
 }
-
-// ---- tile staging ---------------------------------------------------------------------------------------------------
-// A 32-key tile of K and of V lives in LDS row-major (rows of D 16-bit values) with its 16-byte chunks XOR-swizzled
-// per row, so both MFMA operand reads are conflict-free: K chunk c of key k sits at c ^ (k & 7); V chunk c at
-// c ^ 2 (k & 3). 16-bit pages are DMA'd straight into that layout with global_load_lds (lane p of an instruction
-// fills slot p; its source is the chunk the swizzle puts there); fp8 pages are loaded into registers and dequantised
-// into the same layout.
-
-template <int D>
-struct Tile {
-  static constexpr int CH = D / 8;           // 16-byte chunks per row
-  static constexpr int ROWB = 2 * D;         // bytes per row
-  static constexpr int BYTES = kTileKeys * ROWB;
-  static constexpr int RPI = 1024 / ROWB;    // rows one global_load_lds instruction fills (64 lanes x 16 bytes)
-  static constexpr int NI = kTileKeys / RPI;  // instructions per matrix per tile
-  static E4_DEV int kswz(int row) { return row & (CH < 8 ? CH - 1 : 7); }
-  static E4_DEV int vswz(int row) { return (2 * (row & 3)) & (CH - 1); }
-};
 
 // The pages of the rows a wave's direct loads fill (instructions n = wave + NW m), looked up two tiles ahead.
 template <int D, int NW>
@@ -256,11 +199,10 @@ E4_DEV void issue_tile(int tile, char (*smem)[2][Tile<D>::BYTES], int n_ctx, Fp8
 }
 
 template <int D, int NW, typename T, bool FP8>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void verify_attention_kernel(const eagle4_attn_args a, int chunk, int row_tiles,
+__global__ __launch_bounds__(64 * NW) void verify_attention_kernel(const eagle4_attn_args a, int chunk, int row_tiles,
                                                                   int max_splits) {
   static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
   using TL = Tile<D>;
-  typedef short v4i16 __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buffer][K, V]
 
   const int split = blockIdx.x;
@@ -280,14 +222,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const bool row_ok = computes && t < rq.width && t < a.max_query_len;
   const int64_t head = static_cast<int64_t>(kvh) * G + gq;
 
-  // Q of the lane's row: d = 32 c + 8 g + (0..7) for c < D / 32 (the B operand of S^T = K Q^T)
   uint4 qreg[D / 32];
-  {
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + (rq.start + t) * a.stride_qt + head * a.stride_qh + 8 * g;
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c)
-      qreg[c] = row_ok ? *reinterpret_cast<const uint4*>(qp + 32 * c) : make_uint4(0, 0, 0, 0);
-  }
+  load_q<D>(qreg, static_cast<const uint16_t*>(a.q) + (rq.start + t) * a.stride_qt + head * a.stride_qh, row_ok, g);
   const int64_t row_mask = row_ok ? a.masks[b * a.stride_mask + t] : 0;
 
   f32x4_t acc[D / 16];  // O^T: acc[dt][i] is d = 16 dt + 4 g + i of the lane's row
@@ -352,68 +288,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const char* sKb = smem[tile & 1][0];
     const char* sVb = smem[tile & 1][1];
 
-    if (computes) {
-      // ---- S^T = K Q^T for keys 0..15 and 16..31: s[kt][i] is key 16 kt + 4 g + i of the lane's row ----------
-      f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int key = 16 * kt + l16;
-        const char* kr = sKb + key * TL::ROWB;
-#pragma unroll
-        for (int c = 0; c < D / 32; ++c)
-          s[kt] = mfma16<T>(*reinterpret_cast<const uint4*>(kr + 16 * ((4 * c + g) ^ TL::kswz(key))), qreg[c], s[kt]);
-      }
-      // ---- mask, online softmax (log2 domain; 4 lanes share a row) ----------------------------------------------
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = base + 16 * kt + 4 * g + i;
-          const bool ok = is_new ? (key < width && ((row_mask >> key) & 1)) : key < hi;
-          const float v = ok ? s[kt][i] * scale_log2 : -INFINITY;
-          s[kt][i] = v;
-          tmax = fmaxf(tmax, v);
-        }
-      }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-      const float m_new = fmaxf(m, tmax);
-      const float safe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m - safe);
-      float psum = 0.f;
-      uint32_t w[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4
-        const float p0 = exp2f(s[p >> 1][2 * (p & 1)] - safe);
-        const float p1 = exp2f(s[p >> 1][2 * (p & 1) + 1] - safe);
-        psum += p0 + p1;
-        w[p] = pack2<T>(p0, p1);
-      }
-      const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
-      psum += __shfl_xor(psum, 16, 64);
-      psum += __shfl_xor(psum, 32, 64);
-      l = l * alpha + psum;
-      m = m_new;
-      // ---- O^T = O^T * alpha + V^T P^T: V^T operands by transposing LDS reads of the row-major tile ------------
-      const int j = l16 >> 2, s4 = l16 & 3;
-#pragma unroll
-      for (int dt = 0; dt < D / 16; ++dt) {
-        const int lc = 2 * dt + (s4 >> 1), half = 8 * (s4 & 1);
-        const int k0 = 4 * g + j, k1 = 16 + 4 * g + j;
-        const v4i16 lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(sVb + k0 * TL::ROWB + 16 * (lc ^ TL::vswz(k0)) + half));
-        const v4i16 hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4i16*)(sVb + k1 * TL::ROWB + 16 * (lc ^ TL::vswz(k1)) + half));
-        uint4 va;
-        va.x = __builtin_bit_cast(uint2, lo4).x;
-        va.y = __builtin_bit_cast(uint2, lo4).y;
-        va.z = __builtin_bit_cast(uint2, hi4).x;
-        va.w = __builtin_bit_cast(uint2, hi4).y;
-        acc[dt] *= alpha;
-        acc[dt] = mfma16<T>(va, pb, acc[dt]);
-      }
-    }
+    if (computes)
+      tile_step<D, T>(sKb, sVb, qreg, acc, m, l, scale_log2, is_new, base, hi, width, row_mask, g, l16);
     if constexpr (FP8) {  // the next context tile's dequantised K / V into the other buffer (read after the barrier)
       if (tile + 1 < n_ctx) store_fp8<D, NW, T>(smem[(tile + 1) & 1][0], smem[(tile + 1) & 1][1], f8, tid);
     }
@@ -422,22 +298,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   if (!row_ok) return;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   if (rq.splits == 1) {
-    uint16_t* op = static_cast<uint16_t*>(a.out) + (rq.start + t) * a.stride_ot + head * a.stride_oh + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
-      uint2 w;
-      w.x = pack2<T>(acc[dt][0] * inv, acc[dt][1] * inv);
-      w.y = pack2<T>(acc[dt][2] * inv, acc[dt][3] * inv);
-      *reinterpret_cast<uint2*>(op + 16 * dt) = w;
-    }
+    store_rows<D, T>(static_cast<uint16_t*>(a.out) + (rq.start + t) * a.stride_ot + head * a.stride_oh, acc, inv, g);
   } else {
     const int rows = row_tiles * 16;
     const int64_t part = ((static_cast<int64_t>(b) * a.Hkv + kvh) * max_splits + split) * rows + rho;
-    float* pp = a.workspace + part * D + 4 * g;
-#pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt)
-      *reinterpret_cast<float4*>(pp + 16 * dt) =
-          make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+    store_partial<D>(a.workspace + part * D, acc, inv, g);
     if (g == 0) {
       float* lse = a.workspace + static_cast<int64_t>(a.num_reqs) * a.Hkv * max_splits * rows * D;
       lse[part] = l > 0.f ? m + log2f(l) : -INFINITY;
@@ -559,19 +424,27 @@ int launch_d(const eagle4_attn_args& a, const Plan& p, hipStream_t s) {
 
 extern "C" int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* a) {
   if (!covered(*a)) return -1;
+  StreamPlan sp;
+  if (stream_covered(*a) && stream_plan(*a, sp)) return stream_workspace_bytes(sp, *a);
   const Plan p = plan(*a);
   if (p.max_splits <= 1) return 0;
   const int64_t parts = static_cast<int64_t>(a->num_reqs) * a->Hkv * p.max_splits * p.row_tiles * 16;
   return parts * (a->D + 1) * static_cast<int64_t>(sizeof(float));
 }
 
+// 16-bit caches of up to 1024 requests take the streamed schedule; fp8 caches and larger batches the split one.
 extern "C" int eagle4_verify_attention(const eagle4_attn_args* a, void* stream) {
   if (a->num_reqs == 0) return EAGLE4_OK;
   if (!covered(*a)) return EAGLE4_NOT_COVERED;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  StreamPlan sp;
+  if (stream_covered(*a) && stream_plan(*a, sp)) {
+    if (a->workspace == nullptr || a->workspace_bytes < stream_workspace_bytes(sp, *a)) return EAGLE4_NOT_COVERED;
+    return stream_launch(*a, sp, s);
+  }
   const Plan p = plan(*a);
   if (p.max_splits > 1 && (a->workspace == nullptr || a->workspace_bytes < eagle4_verify_attention_workspace(a)))
     return EAGLE4_NOT_COVERED;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (a->D) {
     case 32: return launch_d<32>(*a, p, s);
     case 64: return launch_d<64>(*a, p, s);

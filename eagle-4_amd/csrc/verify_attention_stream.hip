@@ -1,0 +1,711 @@
+// Tree-verify attention over 16-bit paged KV caches, streamed (vllm/verify_attention.py:29-207 computes the same
+// rows; this is its schedule for gfx950).
+//
+// The work is the sequence of 32-key tiles of every segment — (request, KV head, row group), context tiles then
+// draft tiles — in request order. A persistent grid of one workgroup per resident slot takes equal contiguous shares
+// of that sequence, so every CU streams the same number of KV bytes whatever the context lengths are, and no
+// workgroup drains its pipeline between segments. A segment that lies inside one share is normalised and written
+// directly; one cut by share boundaries leaves fp32 partials (with their log2-sum-exp) that a second kernel merges.
+//
+// A workgroup is C consumer waves, each owning 16 query rows (a row is a (draft token, query head of the KV head's
+// group) pair, so one read of a K / V tile serves all G W rows), and two producer waves. The producers run the page
+// lookups and the K / V loads of a kStages-deep LDS ring; iteration x computes tile x while tiles x + 1 .. x + S - 1
+// are in flight (two producers: a wave holds at most 63 loads in flight, fewer than S - 1 tiles' 1 KB loads). Loads
+// and lookups are LDS DMA (global_load_lds) issued from inline assembly: the compiler cannot see them, so it does not
+// drain the load counter before the consumers' LDS reads; each producer waits explicitly — vmcnt(n) with n the loads
+// it issued after the ones tile x needs, exact because vector loads retire in issue order — and a barrier per tile
+// hands the tile over. When a load instruction's rows share one page (page sizes dividing 32
+// or multiples of 32), its address is a scalar page base plus a per-lane constant.
+//
+// Roofline: HBM reads of K and V (2 D bytes per key per KV head and row group); the MFMA work per tile (G W rows
+// against 32 keys) is a fraction of the bf16 ridge, so the design target is bytes in flight.
+
+#include "attention_tile.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"  // the direct loads set M0; no compiler-generated code here uses M0
+
+namespace e4attn {
+
+constexpr int kStages = 4;            // power of two
+constexpr int kProducers = 2;
+constexpr int kMinTilesPerGroup = 8;  // small jobs use fewer, longer shares
+
+namespace {
+
+E4_DEV int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+E4_DEV uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// 64 lanes x 16 bytes from per-lane global addresses into LDS [lds, lds + 1024), lane p at lds + 16 p.
+E4_DEV void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// The same from a scalar base plus per-lane 32-bit offsets.
+E4_DEV void dma16s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// 64 lanes x 4 bytes into LDS [lds, lds + 256).
+E4_DEV void dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+template <int N>
+E4_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Position in the tile sequence: request b, segment k of the request (KV head k / RG, row group k % RG), tile j of
+// the segment; with the request's tile counts, context length, query start and draft width (keys, at most 64).
+struct Cursor {
+  int b, k, j;
+  int tiles, n_ctx, ctx, qs, width;
+};
+
+E4_DEV void cur_load(Cursor& c, const int* s_qsl, const int* s_ctx, int B) {
+  if (c.b >= B) {  // past the last request (a look-ahead cursor): an empty draft tile
+    c.tiles = 1;
+    c.n_ctx = 0;
+    c.ctx = 0;
+    c.qs = 0;
+    c.width = 1;
+    return;
+  }
+  c.qs = uni(s_qsl[c.b]);
+  const int w = uni(s_qsl[c.b + 1]) - c.qs;
+  c.width = w < 64 ? w : 64;
+  c.ctx = uni(s_ctx[c.b]);
+  c.n_ctx = c.width > 0 ? (c.ctx + kTileKeys - 1) / kTileKeys : 0;
+  c.tiles = c.width > 0 ? c.n_ctx + (c.width + kTileKeys - 1) / kTileKeys : 0;
+}
+
+E4_DEV void cur_next(Cursor& c, const int* s_qsl, const int* s_ctx, int B, int HR) {
+  if (++c.j < c.tiles) return;
+  c.j = 0;
+  if (++c.k < HR) return;
+  c.k = 0;
+  do {
+    ++c.b;
+    cur_load(c, s_qsl, s_ctx, B);
+  } while (c.tiles == 0);
+}
+
+E4_DEV int tiles_of(const int* s_qsl, const int* s_ctx, int b) {
+  const int w = s_qsl[b + 1] - s_qsl[b];
+  if (w <= 0) return 0;
+  const int wk = w < 64 ? w : 64;
+  return (s_ctx[b] + kTileKeys - 1) / kTileKeys + (wk + kTileKeys - 1) / kTileKeys;
+}
+
+E4_DEV int64_t active_groups(int64_t tiles_all, int nwg) {
+  const int64_t n = (tiles_all + kMinTilesPerGroup - 1) / kMinTilesPerGroup;
+  return n < nwg ? n : nwg;
+}
+
+E4_DEV int page_div(int pos, int page, int shift) {
+  return shift >= 0 ? pos >> shift : static_cast<int>(static_cast<uint32_t>(pos) / static_cast<uint32_t>(page));
+}
+
+// 16 bytes from LDS byte address `addr`; the transposing 8-byte read (ds_read_b64_tr_b16) at `addr`.
+E4_DEV uint4 lds_load16(uint32_t addr) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)static_cast<uintptr_t>(addr);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+E4_DEV v4i16 lds_tr16(uint32_t addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)static_cast<uintptr_t>(addr));
+}
+
+// Per-lane LDS offsets of a consumer's operand reads within a stage. The swizzles XOR only the low three bits of a
+// 16-byte chunk index, so each read is a base plus an immediate: K chunk 4 c + g of key row 16 kt + l16 sits at
+// kb[kt][c & 1] + 128 (c >> 1); the transposing V reads of d-tile dt (keys 4 g + j and 16 + 4 g + j, j = l16 / 4)
+// at vb[h][dt & 3] + 128 (dt >> 2).
+struct OperandOffsets {
+  uint32_t kb[2][2];
+  uint32_t vb[2][4];
+};
+
+template <int D>
+E4_DEV OperandOffsets operand_offsets(int g, int l16) {
+  using TL = Tile<D>;
+  OperandOffsets o;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = 16 * kt + l16;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) o.kb[kt][e] = key * TL::ROWB + 16 * ((4 * e + g) ^ TL::kswz(key));
+  }
+  const int j = l16 >> 2, s4 = l16 & 3;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int key = 16 * h + 4 * g + j;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      o.vb[h][v] = TL::BYTES + key * TL::ROWB + 16 * ((2 * v + (s4 >> 1)) ^ TL::vswz(key)) + 8 * (s4 & 1);
+  }
+  return o;
+}
+
+// Consumer step: one 32-key tile for a wave's 16 rows (lane l16 of each 16-lane group owns row l16; g = lane / 16).
+//   S^T = K Q^T on v_mfma_f32_16x16x32 (s[kt][i]: key 16 kt + 4 g + i of the lane's row); scores outside `vis`
+//   (bit k: key k of the tile is visible to the row) are -inf. Softmax in the log2 domain against a per-row reference
+//   mref that is raised only when a score exceeds it by more than kSlack (then O^T and the lane's partial sum are
+//   rescaled): probabilities stay below 2^kSlack and the common step has no cross-lane traffic. O^T += V^T P^T with
+//   P^T straight from registers as the B operand and V^T from transposing LDS reads. `stage` is the LDS byte address
+//   of the tile's K (V follows it).
+// The reference's online-softmax step is kernels/online_softmax.py:11-24, over vllm/verify_attention.py:62-112's
+// masked scores; raising the reference lazily changes only fp32 rounding.
+template <int D, typename T>
+E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 (&q)[D / 32], f32x4_t (&acc)[D / 16],
+                         float& mref, float& lsum, float scale_log2, uint32_t vis, int g) {
+  constexpr float kSlack = 16.0f;
+  // operands are read in groups (K: KG chunks per key row, V: VG d-tiles), a compiler fence after each group: at
+  // most two groups are in registers at once (one being multiplied, the next arriving)
+  constexpr int KG = 4, VG = 4;
+  const uint32_t kb[2][2] = {{stage + off.kb[0][0], stage + off.kb[0][1]}, {stage + off.kb[1][0], stage + off.kb[1][1]}};
+  f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int c0 = 0; c0 < D / 32; c0 += KG) {
+    uint4 kop[2][KG];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
+        const int cc = c0 + c;
+        kop[kt][c] = lds_load16(kb[kt][cc & 1] + 128 * (cc >> 1));
+      }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < KG && c0 + c < D / 32; ++c)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(kop[kt][c], q[c0 + c], s[kt]);
+  }
+  auto read_v = [&](int dt) {
+    const uint32_t o = 128 * (dt >> 2);
+    const v4i16 lo4 = lds_tr16(stage + off.vb[0][dt & 3] + o);
+    const v4i16 hi4 = lds_tr16(stage + off.vb[1][dt & 3] + o);
+    return make_uint4(__builtin_bit_cast(uint2, lo4).x, __builtin_bit_cast(uint2, lo4).y,
+                      __builtin_bit_cast(uint2, hi4).x, __builtin_bit_cast(uint2, hi4).y);
+  };
+  uint4 vop[VG];
+#pragma unroll
+  for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);  // the first group lands while the softmax runs
+  asm volatile("" ::: "memory");
+
+  const uint32_t vv = vis >> (4 * g);
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] * scale_log2 : -INFINITY;
+      s[kt][i] = v;
+      tmax = fmaxf(tmax, v);
+    }
+  if (__any(tmax > mref + kSlack)) {  // rare: a new reference for every row of the wave (max over the row's lanes)
+    float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
+    const float m_new = fmaxf(mref, rm);
+    const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mref - m_new);
+    mref = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+  }
+  const float ref = mref == -INFINITY ? 0.f : mref;
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4
+    const float p0 = __builtin_amdgcn_exp2f(s[p >> 1][2 * (p & 1)] - ref);
+    const float p1 = __builtin_amdgcn_exp2f(s[p >> 1][2 * (p & 1) + 1] - ref);
+    lsum += p0 + p1;
+    w[p] = pack2<T>(p0, p1);
+  }
+  const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+  for (int d0 = 0; d0 < D / 16; d0 += VG) {
+    uint4 nxt[VG];
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) nxt[i] = read_v(d0 + VG + i);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(vop[i], pb, acc[d0 + i]);
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) vop[i] = nxt[i];
+    }
+  }
+}
+
+// Visible keys of a tile for one row: context tiles, positions below the context length; draft tiles, draft rows
+// below the width whose ancestor bit the row holds.
+E4_DEV uint32_t visible(bool is_new, int base, int hi, int width, int64_t row_mask) {
+  const int n = is_new ? width - base : hi - base;
+  const uint32_t below = n >= 32 ? 0xffffffffu : (n <= 0 ? 0u : (1u << n) - 1u);
+  return is_new ? below & static_cast<uint32_t>(static_cast<uint64_t>(row_mask) >> base) : below;
+}
+
+// A producer's wait before handing tile x over: the loads it issued after tile x's are `later` tiles of NL direct
+// loads plus, for the producer that runs the page lookups (LK = 1), S - 2 lookups.
+template <int NS, int NL, int LK>
+E4_DEV void wait_producer(int later) {
+  static_assert(NS == 4, "waits written for four stages");
+  constexpr int c0 = LK * (NS - 2), c1 = NL + LK * (NS - 2), c2 = 2 * NL + LK * (NS - 2);
+  static_assert(c2 < 64, "vmcnt field");
+  if (later >= 2)
+    wait_vm<c2>();
+  else if (later == 1)
+    wait_vm<c1>();
+  else
+    wait_vm<c0>();
+}
+
+constexpr int waves_per_eu(int d) { return d == 256 ? 2 : (d == 128 ? 3 : 4); }
+
+// One workgroup: C consumer waves (16 query rows each) and kProducers producer waves (page lookups, direct loads).
+template <int D, int C, typename T>
+__global__ __launch_bounds__(64 * (C + kProducers)) __attribute__((amdgpu_waves_per_eu(waves_per_eu(D))))
+void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
+  static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
+  using TL = Tile<D>;
+  constexpr int NW = C + kProducers;
+  constexpr int NT = 64 * NW;
+  constexpr int NS = kStages;
+  constexpr int NG = TL::NI / kProducers;  // row groups per producer: nn = producer + kProducers i, K then V
+  static_assert(TL::NI % kProducers == 0, "row groups split evenly");
+  __shared__ __attribute__((aligned(1024))) char smem[NS][2][TL::BYTES];  // [stage][K, V]
+  __shared__ __attribute__((aligned(256))) int s_pid[NS][64];             // page ids of a tile's keys
+  __shared__ int s_qsl[kStreamMaxReqs + 1];
+  __shared__ int s_ctx[kStreamMaxReqs];
+  __shared__ int64_t s_wsum[NW];
+  __shared__ int64_t s_start[2];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = uni(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int B = a.num_reqs;
+  const int HR = p.HR;
+
+  // ---- the requests' query starts and (clamped) contexts, and each workgroup's share of the tile sequence ------
+  {
+    const int64_t capacity = static_cast<int64_t>(a.max_blocks) * a.page;
+    for (int i = tid; i <= B; i += NT) s_qsl[i] = static_cast<int>(e4::ld(a.query_start_loc, i));
+    for (int i = tid; i < B; i += NT) {
+      const int64_t c = e4::ld(a.context_lens, i);
+      s_ctx[i] = static_cast<int>(c < 0 ? 0 : (c > capacity ? capacity : c));
+    }
+  }
+  __syncthreads();
+  const int per = (B + NT - 1) / NT;
+  const int b_lo = tid * per < B ? tid * per : B;
+  const int b_hi = b_lo + per < B ? b_lo + per : B;
+  int64_t mine = 0;
+  for (int b = b_lo; b < b_hi; ++b) mine += tiles_of(s_qsl, s_ctx, b);
+  int64_t incl = mine;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t v = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += v;
+  }
+  if (lane == 63) s_wsum[wave] = incl;
+  __syncthreads();
+  int64_t before = incl - mine, total = 0;
+#pragma unroll
+  for (int w2 = 0; w2 < NW; ++w2) {
+    const int64_t v = s_wsum[w2];
+    before += w2 < wave ? v : 0;
+    total += v;
+  }
+  const int64_t tiles_all = total * HR;
+  const int64_t nact = active_groups(tiles_all, p.nwg);
+  const int w = blockIdx.x;
+  const int64_t g0 = nact > 0 ? tiles_all * w / nact : 0;
+  const int64_t g1 = nact > 0 ? tiles_all * (w + 1) / nact : 0;
+  {
+    int64_t* pre = reinterpret_cast<int64_t*>(a.workspace);
+    int64_t run = before;
+    for (int b = b_lo; b < b_hi; ++b) {
+      const int tb = tiles_of(s_qsl, s_ctx, b);
+      if (w == 0) pre[b] = run;
+      if (tb > 0 && run * HR <= g0 && g0 < (run + tb) * HR) {
+        s_start[0] = b;
+        s_start[1] = run;
+      }
+      run += tb;
+    }
+    if (w == 0 && tid == 0) pre[B] = total;
+  }
+  __syncthreads();
+  if (w >= nact || g0 >= g1) return;
+
+  // ---- cursors: compute (cc), direct loads (cd, S - 1 ahead), page lookups (cl, 2 S - 2 ahead) -------------------
+  Cursor cc;
+  {
+    cc.b = uni(static_cast<int>(s_start[0]));
+    cur_load(cc, s_qsl, s_ctx, B);
+    const int64_t off = g0 - s_start[1] * HR;
+    cc.k = uni(static_cast<int>(off / cc.tiles));
+    cc.j = uni(static_cast<int>(off - static_cast<int64_t>(cc.k) * cc.tiles));
+  }
+  const int RG = p.RG;
+
+  if (wave >= C) {  // ---- producers ---------------------------------------------------------------------------------
+    const int pi = wave - C;  // producer 0 also runs the page lookups
+    Cursor cd = cc, cl = cc;
+    const int page = a.page;
+    const int page_shift = (page & (page - 1)) == 0 ? __builtin_ctz(page) : -1;
+    const char* const kcache = static_cast<const char*>(a.key_cache);
+    const char* const vcache = static_cast<const char*>(a.value_cache);
+    const int64_t kb2 = a.stride_kb * 2, ks2 = a.stride_ks * 2, kh2 = a.stride_kh * 2;
+    const int64_t vb2 = a.stride_vb * 2, vs2 = a.stride_vs * 2, vh2 = a.stride_vh * 2;
+    const char* const knew = static_cast<const char*>(a.k_new);
+    const char* const vnew = static_cast<const char*>(a.v_new);
+    const int64_t knt2 = a.stride_knt * 2, knh2 = a.stride_knh * 2, vnt2 = a.stride_vnt * 2, vnh2 = a.stride_vnh * 2;
+    const int32_t* const bt = static_cast<const int32_t*>(a.block_table.ptr);
+    const int32_t* const bt_dummy = static_cast<const int32_t*>(a.query_start_loc.ptr);  // any readable word
+    const int pc = lane % TL::CH, lrow = lane / TL::CH;
+    // direct pages: lane offsets of this producer's row group i (nn = pi + kProducers i) from the start of its page
+    // (pages of 32 keys or more hold the whole tile: the tile's first slot is added to the page base instead)
+    const bool whole = page >= kTileKeys;
+    uint32_t koff[NG], voff[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int r0 = (pi + kProducers * i) * TL::RPI;
+      const int slot_row = (whole ? r0 : (r0 & (page - 1))) + lrow;
+      koff[i] = static_cast<uint32_t>(slot_row * ks2 + 16 * (pc ^ TL::kswz(r0 + lrow)));
+      voff[i] = static_cast<uint32_t>(slot_row * vs2 + 16 * (pc ^ TL::vswz(r0 + lrow)));
+    }
+    const uint32_t kbu = static_cast<uint32_t>(kb2), vbu = static_cast<uint32_t>(vb2);
+
+    // page ids of tile c's keys into ring slot `slot` (draft tiles and look-ahead past the end: a dummy read, so
+    // every iteration issues the same loads)
+    auto lookup = [&](const Cursor& c, int slot) {
+      if (pi != 0) return;
+      const int32_t* src = bt_dummy;
+      if (c.j < c.n_ctx) {
+        const int base = c.j * kTileKeys;
+        const int first = page_div(base, page, page_shift);
+        const int last = page_div(base + kTileKeys - 1 < c.ctx ? base + kTileKeys - 1 : c.ctx - 1, page, page_shift);
+        const int idx = first + lane < last ? first + lane : last;
+        src = bt + static_cast<int64_t>(c.b) * a.block_table.s0 + idx;
+      }
+      dma4(src, uni(lds_addr(s_pid[slot])));
+    };
+    // this producer's share of tile c's K / V into stage `slot`: row groups nn = pi + kProducers i (rows RPI nn ..
+    // RPI nn + RPI - 1), K then V
+    auto load_tile = [&](const Cursor& c, int slot) {
+      const int kvh = c.k / RG;
+      const uint32_t kl = lds_addr(smem[slot][0]), vl = lds_addr(smem[slot][1]);
+      if (c.j < c.n_ctx) {
+        const int base = c.j * kTileKeys;
+        const int first = page_div(base, page, page_shift);
+        const char* const kh = kcache + kvh * kh2;
+        const char* const vh = vcache + kvh * vh2;
+        if (p.direct) {
+          // a row group lies in one page (rows past the context read the last page's slots: in bounds, masked); the
+          // tile's page ids come from one LDS read, lane i holding the id of page first + i
+          const int ids = s_pid[slot][lane];
+          const int in0 = whole ? base - first * page : 0;
+          const char* const kt = kh + in0 * ks2;
+          const char* const vt = vh + in0 * vs2;
+#pragma unroll
+          for (int i = 0; i < NG; ++i) {
+            const int nn = pi + kProducers * i;
+            const int rel = whole ? 0 : (nn * TL::RPI) >> page_shift;  // pages below 32 keys: powers of two
+            const uint32_t pid = static_cast<uint32_t>(__builtin_amdgcn_readlane(ids, rel));
+            dma16s(kt + static_cast<uint64_t>(pid) * kbu, koff[i], uni(kl + nn * 1024));
+            dma16s(vt + static_cast<uint64_t>(pid) * vbu, voff[i], uni(vl + nn * 1024));
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < NG; ++i) {
+            const int nn = pi + kProducers * i;
+            const int row = nn * TL::RPI + lrow;
+            const int pos = base + row < c.ctx ? base + row : c.ctx - 1;  // past the context: its last key (masked)
+            const int pg = page_div(pos, page, page_shift);
+            const int64_t pid = s_pid[slot][pg - first];
+            const int64_t sl = pos - pg * page;
+            const char* ksrc = kh + pid * kb2 + sl * ks2 + 16 * (pc ^ TL::kswz(row));
+            const char* vsrc = vh + pid * vb2 + sl * vs2 + 16 * (pc ^ TL::vswz(row));
+            dma16(ksrc, uni(kl + nn * 1024));
+            dma16(vsrc, uni(vl + nn * 1024));
+          }
+        }
+      } else {
+        const int base = (c.j - c.n_ctx) * kTileKeys;
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+          const int nn = pi + kProducers * i;
+          const int row = nn * TL::RPI + lrow;
+          const int key = base + row < c.width ? base + row : c.width - 1;  // past the draft rows: the last (masked)
+          const int64_t tok = c.qs + key;
+          const char* ksrc = knew + tok * knt2 + kvh * knh2 + 16 * (pc ^ TL::kswz(row));
+          const char* vsrc = vnew + tok * vnt2 + kvh * vnh2 + 16 * (pc ^ TL::vswz(row));
+          dma16(ksrc, uni(kl + nn * 1024));
+          dma16(vsrc, uni(vl + nn * 1024));
+        }
+      }
+    };
+
+    // prologue (kStages barriers, matched by the consumers): lookups of the first S - 1 tiles, landed before any
+    // producer reads them; then those tiles' loads interleaved with the next lookups in the steady state's order, a
+    // barrier after each step (a lookup reuses the ring slot that both producers read in the step before)
+    for (int i = 0; i < NS - 1; ++i) {
+      lookup(cl, static_cast<int>((g0 + i) & (NS - 1)));
+      cur_next(cl, s_qsl, s_ctx, B, HR);
+    }
+    wait_vm<0>();
+    __syncthreads();
+    for (int i = 0; i < NS - 1; ++i) {
+      if (g0 + i < g1) load_tile(cd, static_cast<int>((g0 + i) & (NS - 1)));
+      cur_next(cd, s_qsl, s_ctx, B, HR);
+      lookup(cl, static_cast<int>((g0 + NS - 1 + i) & (NS - 1)));
+      cur_next(cl, s_qsl, s_ctx, B, HR);
+      __syncthreads();
+    }
+    for (int64_t x = g0; x < g1; ++x) {
+      const int slot = static_cast<int>(x & (NS - 1));
+      const int64_t left = g1 - x - 1;
+      const int later = static_cast<int>(left < NS - 2 ? left : NS - 2);
+      if (pi == 0)
+        wait_producer<NS, 2 * NG, 1>(later);
+      else
+        wait_producer<NS, 2 * NG, 0>(later);
+      __syncthreads();  // tile x is in LDS; stage x - 1 has been read by every consumer
+      if (x + NS - 1 < g1) load_tile(cd, (slot + NS - 1) & (NS - 1));
+      cur_next(cd, s_qsl, s_ctx, B, HR);
+      lookup(cl, (slot + 2 * NS - 2) & (NS - 1));
+      cur_next(cl, s_qsl, s_ctx, B, HR);
+    }
+    wait_vm<0>();
+    return;
+  }
+
+  // ---- consumers ---------------------------------------------------------------------------------------------------
+  const int G = p.G;
+  const float scale_log2 = a.scale * 1.4426950408889634f;
+  uint4 q[D / 32];
+  int64_t row_mask = 0;
+  bool row_ok = false;
+  int t = 0, head = 0;
+  // the segment's row of this lane: Q, ancestor mask
+  auto enter = [&](const Cursor& c) {
+    const int kvh = c.k / RG, rg = c.k - kvh * RG;
+    const int rows = c.width < a.max_query_len ? c.width : a.max_query_len;
+    const int rt = rg * C + wave;
+    const int rho = rt * 16 + l16;
+    t = rho / G;
+    head = kvh * G + (rho - t * G);
+    row_ok = rt < p.row_tiles && t < rows;
+    load_q<D>(q, static_cast<const uint16_t*>(a.q) + (c.qs + t) * a.stride_qt + head * a.stride_qh, row_ok, g);
+    row_mask = row_ok ? a.masks[static_cast<int64_t>(c.b) * a.stride_mask + t] : 0;
+  };
+  enter(cc);
+  f32x4_t acc[D / 16];
+  float mref, lsum;
+  auto reset = [&] {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    mref = -INFINITY;
+    lsum = 0.f;
+  };
+  reset();
+  const OperandOffsets off = operand_offsets<D>(g, l16);
+  int piece_j0 = cc.j;
+  const int rows_seg = p.rows_seg;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) __syncthreads();  // the producers' prologue
+
+  for (int64_t x = g0; x < g1; ++x) {
+    const int slot = static_cast<int>(x & (NS - 1));
+    __syncthreads();
+    const bool is_new = cc.j >= cc.n_ctx;
+    const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * kTileKeys;
+    consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
+                       visible(is_new, base, cc.ctx, cc.width, row_mask), g);
+
+    const bool seg_end = cc.j == cc.tiles - 1;
+    if (seg_end || x == g1 - 1) {
+      float ls = lsum + __shfl_xor(lsum, 16, 64);
+      ls += __shfl_xor(ls, 32, 64);
+      if (row_ok) {
+        const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+        if (piece_j0 == 0 && seg_end) {
+          store_rows<D, T>(static_cast<uint16_t*>(a.out) + (cc.qs + t) * a.stride_ot + head * a.stride_oh, acc, inv,
+                           g);
+        } else {
+          const int64_t part = (static_cast<int64_t>(cc.b) * HR + cc.k + w) * rows_seg + 16 * wave + l16;
+          store_partial<D>(a.workspace + p.part_off + part * D, acc, inv, g);
+          if (g == 0) a.workspace[p.lse_off + part] = ls > 0.f ? mref + log2f(ls) : -INFINITY;
+        }
+      }
+      if (x + 1 < g1) {
+        cur_next(cc, s_qsl, s_ctx, B, HR);
+        enter(cc);
+        reset();
+        piece_j0 = 0;
+      }
+    } else {
+      ++cc.j;
+    }
+  }
+}
+
+// Merges the pieces of each segment cut by share boundaries (vllm/verify_attention.py:115-139): weights
+// 2^(lse_i - max) over the pieces' normalised fp32 partials. One workgroup per segment.
+template <int D, typename T>
+__global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_args a, const StreamPlan p) {
+  const int s = blockIdx.x;
+  const int b = s / p.HR, k = s - b * p.HR;
+  const int64_t* pre = reinterpret_cast<const int64_t*>(a.workspace);
+  const int64_t tiles = pre[b + 1] - pre[b];
+  if (tiles <= 0) return;
+  const int64_t tiles_all = pre[a.num_reqs] * p.HR;
+  const int64_t nact = active_groups(tiles_all, p.nwg);
+  const int64_t start = pre[b] * p.HR + k * tiles, end = start + tiles;
+  const int64_t w0 = ((start + 1) * nact - 1) / tiles_all, w1 = (end * nact - 1) / tiles_all;
+  if (w0 == w1) return;  // inside one share: written directly
+  const int G = p.G, kvh = k / p.RG, rg = k - kvh * p.RG;
+  const int rows_seg = p.rows_seg;
+  const int64_t qs = e4::ld(a.query_start_loc, b);
+  int64_t rows = e4::ld(a.query_start_loc, b + 1) - qs;
+  rows = rows < a.max_query_len ? rows : a.max_query_len;
+  constexpr int TPR = D / 4;
+  for (int item = threadIdx.x; item < rows_seg * TPR; item += 256) {
+    const int r = item / TPR, d = 4 * (item % TPR);
+    const int rho = rg * rows_seg + r;
+    const int rt = rho / 16;
+    const int t = rho / G, gq = rho - t * G;
+    if (rt >= p.row_tiles || t >= rows) continue;
+    float mx = -INFINITY;
+    for (int64_t wi = w0; wi <= w1; ++wi) mx = fmaxf(mx, a.workspace[p.lse_off + (s + wi) * rows_seg + r]);
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    float wsum = 0.f;
+    for (int64_t wi = w0; wi <= w1; ++wi) {
+      const int64_t part = (s + wi) * rows_seg + r;
+      const float ls = a.workspace[p.lse_off + part];
+      const float wt = ls == -INFINITY ? 0.f : exp2f(ls - mx);
+      const float4 v = *reinterpret_cast<const float4*>(a.workspace + p.part_off + part * D + d);
+      sum.x += wt * v.x;
+      sum.y += wt * v.y;
+      sum.z += wt * v.z;
+      sum.w += wt * v.w;
+      wsum += wt;
+    }
+    const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+    uint2 o;
+    o.x = pack2<T>(sum.x * inv, sum.y * inv);
+    o.y = pack2<T>(sum.z * inv, sum.w * inv);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + (qs + t) * a.stride_ot +
+                              (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d) = o;
+  }
+}
+
+template <int D, int C, typename T>
+int resident_groups() {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(verify_stream_kernel<D, C, T>),
+                                                     64 * (C + kProducers), 0) != hipSuccess)
+      n = 0;
+    return n;
+  }();
+  int dev = 0, cus = 0;
+  if (per_cu <= 0 || hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 0;
+  return per_cu * cus;
+}
+
+// consumer counts instantiated: 2, 4 and 6 waves (a group of row tiles takes the smallest that holds it)
+template <int D, typename T>
+int groups_c(int c) {
+  switch (c) {
+    case 2: return resident_groups<D, 2, T>();
+    case 4: return resident_groups<D, 4, T>();
+    default: return resident_groups<D, 6, T>();
+  }
+}
+
+int groups(const eagle4_attn_args& a, int c) {
+  const bool bf = a.dtype == EAGLE4_BF16;
+  switch (a.D) {
+    case 32: return bf ? groups_c<32, e4::Bf16>(c) : groups_c<32, e4::F16>(c);
+    case 64: return bf ? groups_c<64, e4::Bf16>(c) : groups_c<64, e4::F16>(c);
+    case 128: return bf ? groups_c<128, e4::Bf16>(c) : groups_c<128, e4::F16>(c);
+    default: return bf ? groups_c<256, e4::Bf16>(c) : groups_c<256, e4::F16>(c);
+  }
+}
+
+template <int D, int C, typename T>
+int launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
+  verify_stream_kernel<D, C, T><<<p.nwg, 64 * (C + kProducers), 0, s>>>(a, p);
+  verify_stream_merge<D, T><<<a.num_reqs * p.HR, 256, 0, s>>>(a, p);
+  return E4_LAUNCH_STATUS();
+}
+
+template <int D, typename T>
+int launch_c(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
+  switch (p.C) {
+    case 2: return launch<D, 2, T>(a, p, s);
+    case 4: return launch<D, 4, T>(a, p, s);
+    default: return launch<D, 6, T>(a, p, s);
+  }
+}
+
+}  // namespace
+
+// 16-bit caches (the same dtype as q) and at most kStreamMaxReqs requests; the rest of the contract is checked by
+// the caller.
+bool stream_covered(const eagle4_attn_args& a) {
+  return a.cache_dtype == a.dtype && a.num_reqs <= kStreamMaxReqs;
+}
+
+bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
+  p.G = a.Hq / a.Hkv;
+  p.row_tiles = e4::ceil_div(static_cast<int64_t>(p.G) * a.max_query_len, 16);
+  p.RG = e4::ceil_div(p.row_tiles, 6);
+  const int need = e4::ceil_div(p.row_tiles, p.RG);
+  p.C = need <= 2 ? 2 : (need <= 4 ? 4 : 6);
+  p.HR = a.Hkv * p.RG;
+  p.rows_seg = 16 * p.C;
+  // direct page addressing: every direct-load instruction's rows (1024 / (2 D) consecutive keys) in one page, a
+  // page's slots addressable by 32-bit lane offsets, block strides below 4 GB
+  const int rpi = 512 / a.D;
+  const bool aligned = a.page % kTileKeys == 0 || (kTileKeys % a.page == 0 && a.page >= rpi);
+  const int64_t span = static_cast<int64_t>(a.page) * (a.stride_ks > a.stride_vs ? a.stride_ks : a.stride_vs) * 2;
+  const int64_t block_bytes = 2 * (a.stride_kb > a.stride_vb ? a.stride_kb : a.stride_vb);
+  p.direct = aligned && a.stride_ks >= 0 && a.stride_vs >= 0 && a.stride_kb >= 0 && a.stride_vb >= 0 &&
+             span < (int64_t(1) << 31) && block_bytes < (int64_t(1) << 32);
+  p.nwg = groups(a, p.C);
+  if (p.nwg <= 0) return false;
+  const int64_t slots = static_cast<int64_t>(a.num_reqs) * p.HR + p.nwg;
+  const int64_t rows_seg = p.rows_seg;
+  p.part_off = (2 * (static_cast<int64_t>(a.num_reqs) + 1) + 63) / 64 * 64;
+  p.lse_off = p.part_off + slots * rows_seg * a.D;
+  return true;
+}
+
+int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args& a) {
+  const int64_t slots = static_cast<int64_t>(a.num_reqs) * p.HR + p.nwg;
+  return (p.lse_off + slots * p.rows_seg) * static_cast<int64_t>(sizeof(float));
+}
+
+int stream_launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
+  const bool bf = a.dtype == EAGLE4_BF16;
+  switch (a.D) {
+    case 32: return bf ? launch_c<32, e4::Bf16>(a, p, s) : launch_c<32, e4::F16>(a, p, s);
+    case 64: return bf ? launch_c<64, e4::Bf16>(a, p, s) : launch_c<64, e4::F16>(a, p, s);
+    case 128: return bf ? launch_c<128, e4::Bf16>(a, p, s) : launch_c<128, e4::F16>(a, p, s);
+    default: return bf ? launch_c<256, e4::Bf16>(a, p, s) : launch_c<256, e4::F16>(a, p, s);
+  }
+}
+
+}  // namespace e4attn

@@ -34,6 +34,34 @@ def _want(inp, fp8=False):
                                inp["scale"], out, max_query_len=inp["max_query_len"], **kw)
 
 
+def _inputs(contexts, parents, heads, kv_heads, d, page, dtype, seed):
+    """Paged caches with permuted blocks, draft rows, and the trees' ancestor masks; two spare rows past the batch."""
+    gen = torch.Generator().manual_seed(seed)
+    num_reqs = len(contexts)
+    widths = [len(p) for p in parents]
+    width = max(max(widths), 1)
+    max_blocks = max(c // page + 1 for c in contexts) + 1
+    num_blocks = num_reqs * max_blocks + 3
+    kv = torch.randn(num_blocks, page, kv_heads, 2 * d, generator=gen).to(dtype)
+    key_cache, value_cache = kv[..., :d], kv[..., d:]
+    table = torch.randperm(num_blocks, generator=gen)[: num_reqs * max_blocks].view(num_reqs, max_blocks).int()
+    tokens = sum(widths)
+    return dict(
+        q=torch.randn(tokens + 2, heads, d, generator=gen).to(dtype),
+        k_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
+        v_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
+        key_cache=key_cache, value_cache=value_cache, block_table=table,
+        context_lens=torch.tensor(contexts, dtype=torch.int32),
+        query_start_loc=torch.tensor([0] + [sum(widths[: i + 1]) for i in range(num_reqs)], dtype=torch.int32),
+        masks=torch.tensor([tree_masks(p, width) if p else [0] * width for p in parents], dtype=torch.int64),
+        scale=d**-0.5, max_query_len=width,
+    )
+
+
+def _random_parents(gen, width):
+    return [-1] + [int(torch.randint(0, r, (1,), generator=gen)) for r in range(1, width)] if width else []
+
+
 def _close(got, want):
     torch.testing.assert_close(got.float(), want.float(), atol=2e-2, rtol=1e-2)
 
@@ -52,26 +80,8 @@ def _close(got, want):
 def test_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, page, dtype):
     """The reference test's cases (tests/test_verify_attention.py:31-92) plus wider heads and pages."""
     announce(f"attention contexts={contexts} heads={heads}/{kv_heads} d={d} page={page} {dtype}")
-    gen = torch.Generator().manual_seed(len(contexts) * 100 + heads)
-    num_reqs = len(contexts)
-    widths = [len(p) for p in parents]
-    width = max(widths)
-    max_blocks = max(c // page + 1 for c in contexts) + 1
-    num_blocks = num_reqs * max_blocks + 3
-    kv = torch.randn(num_blocks, page, kv_heads, 2 * d, generator=gen).to(dtype)
-    key_cache, value_cache = kv[..., :d], kv[..., d:]
-    table = torch.randperm(num_blocks, generator=gen)[: num_reqs * max_blocks].view(num_reqs, max_blocks).int()
-    tokens = sum(widths)
-    inp = dict(
-        q=torch.randn(tokens + 2, heads, d, generator=gen).to(dtype),
-        k_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
-        v_new=torch.randn(tokens + 2, kv_heads, d, generator=gen).to(dtype),
-        key_cache=key_cache, value_cache=value_cache, block_table=table,
-        context_lens=torch.tensor(contexts, dtype=torch.int32),
-        query_start_loc=torch.tensor([0] + [sum(widths[: i + 1]) for i in range(num_reqs)], dtype=torch.int32),
-        masks=torch.tensor([tree_masks(p, width) for p in parents], dtype=torch.int64),
-        scale=d**-0.5, max_query_len=width,
-    )
+    inp = _inputs(contexts, parents, heads, kv_heads, d, page, dtype, seed=len(contexts) * 100 + heads)
+    tokens = sum(len(p) for p in parents)
     want = _want(inp)
     for chunk in (0, 64, 256):  # one split, many splits, the default
         got = _run(dev, inp, dtype, chunk=chunk)
@@ -138,3 +148,40 @@ def test_fp8_dequant_is_ocp_e4m3(dev):
                          1.0, out, max_query_len=1, k_scale=scale.to(dev), v_scale=scale.to(dev))
         torch.cuda.synchronize()
         torch.testing.assert_close(out[0, 0].cpu().float(), want_vals[kpos].to(torch.bfloat16).float(), atol=0, rtol=0)
+
+
+def test_ragged_batch_with_empty_requests(dev):
+    """40 requests: contexts 0..2500, tree widths 0..24 (empty requests between others), heads 8 / 2, D 128: the
+    streamed schedule's shares cut segments anywhere, so direct and merged rows both occur."""
+    announce("attention ragged 40 requests")
+    gen = torch.Generator().manual_seed(11)
+    contexts = [int(x) for x in torch.randint(0, 2500, (40,), generator=gen)]
+    contexts[3] = 0
+    widths = [int(x) for x in torch.randint(0, 25, (40,), generator=gen)]
+    widths[0], widths[7], widths[39] = 0, 1, 0
+    parents = [_random_parents(gen, w) for w in widths]
+    inp = _inputs(contexts, parents, 8, 2, 128, 16, torch.bfloat16, seed=12)
+    tokens = sum(widths)
+    got = _run(dev, inp, torch.bfloat16)
+    _close(got[:tokens], _want(inp)[:tokens])
+    assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))
+
+
+def test_one_long_request_spans_every_group(dev):
+    """One request with a 60000-key context (heads 8 / 1, D 128): its single segment is cut into one piece per
+    workgroup, all merged."""
+    announce("attention one request l60000")
+    parents = [[-1, 0, 0, 1, 2, 2, 5, 6]]
+    inp = _inputs([60000], parents, 8, 1, 128, 16, torch.bfloat16, seed=13)
+    _close(_run(dev, inp, torch.bfloat16)[:8], _want(inp)[:8])
+
+
+def test_more_requests_than_the_streamed_schedule_holds(dev):
+    """1030 requests (above the streamed schedule's 1024) take the split-context schedule with 16-bit pages."""
+    announce("attention 1030 requests")
+    gen = torch.Generator().manual_seed(14)
+    contexts = [int(x) for x in torch.randint(0, 90, (1030,), generator=gen)]
+    parents = [_random_parents(gen, int(w)) for w in torch.randint(1, 4, (1030,), generator=gen)]
+    inp = _inputs(contexts, parents, 2, 1, 32, 16, torch.bfloat16, seed=15)
+    tokens = sum(len(p) for p in parents)
+    _close(_run(dev, inp, torch.bfloat16)[:tokens], _want(inp)[:tokens])
