@@ -188,43 +188,81 @@ def main() -> int:
 
     names = ["stage", "attention", "conv", "recurrence", "commit"]
 
-    def step(ev=None):
-        def mark(i):
-            if ev is not None:
-                ev[i].record()
-
-        mark(0)
+    def run_stage():
         stage.stage(store, idx, qsl, qsl, positions, B, tokens, tree=True)
-        mark(1)
+
+    def run_attention():
         verify_attention(att["q"], att["k_new"], att["v_new"], att["key_cache"], att["value_cache"],
                          att["block_table"], stage.context_lens[:B], qsl, stage.masks[:B], att["scale"], out,
                          max_query_len=W, chunk=args.chunk)
-        mark(2)
+
+    def run_conv():
         gdn_tree_conv1d_update(gdn["x"].t()[None], gdn["conv_state"], gdn["conv_weight"], None, "silu", slots0, None,
                                None, stage.ancestors[:B], pad_slot_id=0, out=conv_out.t()[None],
                                num_accepted_tokens=gdn["num_accepted"], query_start_loc=qsl)
-        mark(3)
+
+    def run_recurrence():
         gdn_tree_recurrent_update(gdn["A_log"], gdn["dt_bias"], q4, k4, v4, gdn["a"], gdn["b"],
                                   initial_state_source=gdn["pool"], initial_state_indices=gdn["slots"],
                                   cu_seqlens=qsl, intermediate_states_buffer=gdn["pool"],
                                   intermediate_state_indices=gdn["slots"], retrieve_parent_token=stage.parents[:B],
                                   num_accepted_tokens=gdn["num_accepted"], pad_slot_id=0, out=rec_out)
-        mark(4)
+
+    def run_commit():
         commit.commit(idx, path_d, path_len_d)
-        mark(5)
         positions.copy_(chain_pos)  # the next round's chain positions (the stage rewrites them to depths)
+
+    parts = dict(stage=run_stage, attention=run_attention, conv=run_conv, recurrence=run_recurrence,
+                 commit=run_commit)
+
+    def step():
+        for n in names:
+            parts[n]()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step(events[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per = {n: sum(events[i][j].elapsed_time(events[i][j + 1]) for i in range(args.steps)) / args.steps
-           for j, n in enumerate(names)}
+
+    # A step is replayed as one HIP graph (the launches of a verify round, as a serving loop issues them), so the
+    # timing is the GPU's, not the host's Python. Each kernel's own duration comes from a graph of that kernel alone,
+    # replayed back to back between events on the replay stream.
+    def graph_of(fn):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        return g
+
+    def timed(fn, n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / n  # ms
+
+    timing = "hip-graph replay"
+    try:
+        g_step = graph_of(step)
+        g_parts = {n: graph_of(parts[n]) for n in names}
+        for _ in range(args.warmup):
+            g_step.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            g_step.replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = {n: timed(g_parts[n].replay, args.steps) for n in names}
+    except RuntimeError as err:  # capture unavailable: eager launches (host time between launches included)
+        timing = f"eager ({err.__class__.__name__}: graph capture failed)"
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        per = {n: timed(parts[n], args.steps) for n in names}
     ctx = att["context_lens"].cpu().tolist()
     nbytes = _algorithmic_bytes(B, W, dict(hq=ATTN_B64.hq, hkv=ATTN_B64.hkv, d=ATTN_B64.d, page=ATTN_B64.page),
                                 dict(h=H, hv=HV, k=K, v=V, dim=gdn["dim"]), ctx, path_len.tolist(), path_last)
@@ -256,6 +294,7 @@ def main() -> int:
                         "layer (tree conv1d + snapshot walk H16/HV32 K=V=128 fp32 states + accepted-path commit)",
             "batch": B, "tree_nodes": W, "attention_chunk": args.chunk,
             "step_hbm_bytes": step_bytes, "step_frac_of_hbm_roofline": step_bytes / (wall / args.steps) / HBM_PEAK,
+            "timing": timing,
         },
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic},

@@ -1,64 +1,86 @@
 // Width-4 tree causal conv1d of a GDN verify on gfx950 (kernels/gdn_tree_conv.py:402-497).
 //
-// HBM-bound: per request it streams the nodes' inputs once, writes the outputs (and the windows) once, and touches
-// three history columns plus the rolled state. One thread owns VEC adjacent channels of one request: its history
-// columns stay in registers, every node's window is gathered through the ancestor table (three re-reads of an
-// earlier node's row, L1/L2 hits), and the state roll is written as the nodes go (all history reads happen first).
-// With unit channel stride VEC = 8 and every x / out access is one 16-byte load or store per node.
+// HBM-bound: per request it reads the nodes' inputs, the history columns of the conv state and the weights once,
+// and writes the outputs, the windows and the rolled state once. One workgroup takes one request and a block of
+// kChannels channels. It stages the block's node inputs (token-major, 16 bytes per 8 channels), the ancestor codes,
+// the weights and the history in LDS; every thread then computes the outputs of its 8 channels for a strided set of
+// nodes, each window gathered from LDS through the ancestor table; the state roll is written after a barrier.
+//
+// When the state rows are contiguous (token stride 1, channel stride = state length: the block's rows are one
+// 16-byte-aligned span) the whole span is copied into LDS, rolled there and written back with 16-byte stores, so no
+// cache line is left partly written; otherwise the roll is written element by element along the contiguous
+// dimension. LDS is sized at launch for the widest tree and the state length.
 
 #include "common.h"
 
 namespace {
 
-template <typename T, int VEC>
-struct Vec {
-  typename T::storage v[VEC];
+constexpr int kChannels = 128;          // channels per workgroup
+constexpr int kVecs = kChannels / 8;    // 8-channel vectors per node
+constexpr int kThreads = 256;
+constexpr int kTokLanes = kThreads / kVecs;  // nodes computed concurrently
+constexpr int kMaxNodes = 64;
+constexpr int kMaxRowSpan = 96;         // state length of the LDS roll
+
+// One product of the upstream conv: 16-bit operands, product rounded (nearest even, v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32) to the 16-bit dtype, returned as fp32 (kernels/gdn_tree_conv.py:225-229, 429-430).
+template <typename T>
+E4_DEV float product(uint16_t x, uint16_t w) {
+  const float p = T::to_f32(x) * T::to_f32(w);
+  if constexpr (T::code == EAGLE4_BF16)
+    return static_cast<float>(static_cast<__bf16>(p));
+  else
+    return static_cast<float>(static_cast<_Float16>(p));
+}
+
+// x sigmoid(x) = x / (1 + e^-x), e^-x as 2^(-x log2 e) on v_exp_f32 and the quotient on v_rcp_f32.
+E4_DEV float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+
+E4_DEV uint16_t lane16(const uint4& v, int i) {
+  const uint32_t w = i < 4 ? (i < 2 ? v.x : v.y) : (i < 6 ? v.z : v.w);
+  return static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// LDS layout (byte offsets): node inputs [seqlen][kVecs] x 16, state rows [kChannels][state_len] x 2 (row roll
+// only), history [3][kChannels] x 2, weights [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes [3][seqlen].
+struct Lds {
+  int xs, rows, hist, wts, bias, anc, total;
+  int row_roll;
 };
 
-template <typename T, int VEC>
-E4_DEV void load_vec(Vec<T, VEC>& out, const typename T::storage* p, int64_t stride, bool contiguous, int n) {
-  if constexpr (VEC == 8) {
-    if (contiguous) {
-      const uint4 raw = *reinterpret_cast<const uint4*>(p);
-      const uint16_t* h = reinterpret_cast<const uint16_t*>(&raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) out.v[i] = h[i];
-      return;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) out.v[i] = i < n ? p[i * stride] : typename T::storage(0);
+Lds lds_layout(const eagle4_conv_args& a) {
+  auto up16 = [](int b) { return (b + 15) / 16 * 16; };
+  Lds l;
+  l.row_roll = a.stride_cs_tok == 1 && a.stride_cs_dim == a.state_len && a.state_len <= kMaxRowSpan &&
+               a.dim % kChannels == 0 && (reinterpret_cast<uintptr_t>(a.conv_state) & 15) == 0 &&
+               (a.stride_cs_seq * 2) % 16 == 0;
+  l.xs = 0;
+  l.rows = up16(a.seqlen * kVecs * 16);
+  l.hist = l.rows + (l.row_roll ? up16(kChannels * a.state_len * 2) : 0);
+  l.wts = l.hist + up16(3 * kChannels * 2);
+  l.bias = l.wts + up16(4 * kChannels * 2);
+  l.anc = l.bias + kChannels * 4;
+  l.total = l.anc + up16(3 * a.seqlen * 4);
+  return l;
 }
 
-template <typename T, int VEC>
-E4_DEV void store_vec(typename T::storage* p, int64_t stride, bool contiguous, const Vec<T, VEC>& in) {
-  if constexpr (VEC == 8) {
-    if (contiguous) {
-      uint4 raw;
-      uint16_t* h = reinterpret_cast<uint16_t*>(&raw);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) h[i] = in.v[i];
-      *reinterpret_cast<uint4*>(p) = raw;
-      return;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) p[i * stride] = in.v[i];
-}
-
-// One product of the upstream conv: 16-bit operands, product rounded to the 16-bit dtype, returned as fp32
-// (kernels/gdn_tree_conv.py:225-229, 429-430).
 template <typename T>
-E4_DEV float product(typename T::storage x, typename T::storage w) {
-  return e4::round_through<T>(T::to_f32(x) * T::to_f32(w));
-}
-
-template <typename T, int VEC>
-__global__ __launch_bounds__(256) void tree_conv_kernel(const eagle4_conv_args a) {
-  using S = typename T::storage;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  uint4* const xs = reinterpret_cast<uint4*>(lds + off.xs);        // [t * kVecs + v]
+  uint16_t* const rows = reinterpret_cast<uint16_t*>(lds + off.rows);  // [c * state_len + col]
+  uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c]
+  uint16_t* const wts = reinterpret_cast<uint16_t*>(lds + off.wts);    // [j * kChannels + c]
+  float* const bias_s = reinterpret_cast<float*>(lds + off.bias);
+  int* const anc = reinterpret_cast<int*>(lds + off.anc);             // [j * n + t]
   const int seq = blockIdx.y;
-  const int c0 = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
-  if (c0 >= a.dim) return;
+  const int cb = blockIdx.x * kChannels;
+  const int tid = threadIdx.x;
+  const int L = a.state_len;
+
   // _conv_request (:43-56)
   const int64_t slot = e4::ld(a.conv_state_indices, seq);
   int64_t bos = 0, num_tokens = a.seqlen, history = 0;
@@ -68,91 +90,163 @@ __global__ __launch_bounds__(256) void tree_conv_kernel(const eagle4_conv_args a
   }
   if (a.num_accepted.ptr != nullptr) history = e4::ld(a.num_accepted, seq) - 1;
   if (!(slot > a.pad_slot_id && num_tokens > 0)) return;
-  const int nvec = (a.dim - c0) < VEC ? (a.dim - c0) : VEC;  // a ragged last vector runs the scalar path
-  const bool xc = a.stride_x_dim == 1 && nvec == VEC && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
-                  ((a.stride_x_token | a.stride_x_seq) & 7) == 0 && (c0 & 7) == 0;
-  const bool oc = a.stride_o_dim == 1 && nvec == VEC && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-                  ((a.stride_o_token | a.stride_o_seq) & 7) == 0 && (c0 & 7) == 0;
+  const int n = static_cast<int>(num_tokens < a.seqlen ? num_tokens : a.seqlen);
+  const int nch = a.dim - cb < kChannels ? a.dim - cb : kChannels;
 
-  const S* x = static_cast<const S*>(a.x) + (a.query_start_loc.ptr != nullptr ? 0 : seq * a.stride_x_seq) +
-               bos * a.stride_x_token + c0 * a.stride_x_dim;
-  S* out = static_cast<S*>(a.out) + (a.query_start_loc.ptr != nullptr ? 0 : seq * a.stride_o_seq) +
-           bos * a.stride_o_token + c0 * a.stride_o_dim;
-  S* state = static_cast<S*>(a.conv_state) + slot * a.stride_cs_seq + c0 * a.stride_cs_dim;
-  const S* w = static_cast<const S*>(a.weight) + c0 * a.stride_w_dim;
+  const uint16_t* x = static_cast<const uint16_t*>(a.x) +
+                      (a.query_start_loc.ptr != nullptr ? 0 : seq * a.stride_x_seq) + bos * a.stride_x_token +
+                      static_cast<int64_t>(cb) * a.stride_x_dim;
+  uint16_t* out = static_cast<uint16_t*>(a.out) + (a.query_start_loc.ptr != nullptr ? 0 : seq * a.stride_o_seq) +
+                  bos * a.stride_o_token + static_cast<int64_t>(cb) * a.stride_o_dim;
+  uint16_t* state = static_cast<uint16_t*>(a.conv_state) + slot * a.stride_cs_seq +
+                    static_cast<int64_t>(cb) * a.stride_cs_dim;
 
-  float wt[4][VEC], bias[VEC];
-  S col[3][VEC];
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const bool ok = i < nvec;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wt[j][i] = ok ? T::to_f32(w[i * a.stride_w_dim + j * a.stride_w_width]) : 0.f;
-    bias[i] = (ok && a.bias != nullptr) ? e4::load_scalar(a.bias, c0 + i, a.bias_dtype) : 0.f;
-#pragma unroll
-    for (int j = 0; j < 3; ++j) col[j][i] = ok ? state[i * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : S(0);
-  }
-  // weights as 16-bit operands of the rounded products
-  S wq[4][VEC];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) wq[j][i] = T::from_f32(wt[j][i]);
-
-  const int32_t* anc = a.ancestors + static_cast<int64_t>(seq) * 3 * a.seqlen;
-  const int64_t shift = (num_tokens + 2 < a.state_len ? num_tokens + 2 : a.state_len) - num_tokens - 3;
-  S* window = nullptr;
-  if (a.window != nullptr)
-    window = static_cast<S*>(a.window) + e4::ld(a.window_indices, seq) * a.stride_win_seq + c0 * a.stride_win_dim;
-
-  for (int64_t t = 0; t < num_tokens; ++t) {
-    Vec<T, VEC> xs, v[3];
-    load_vec<T, VEC>(xs, x + t * a.stride_x_token, a.stride_x_dim, xc, nvec);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int code = anc[j * a.seqlen + t];
-      if (code >= 0) {
-        load_vec<T, VEC>(v[j], x + static_cast<int64_t>(code) * a.stride_x_token, a.stride_x_dim, xc, nvec);
-      } else {
-        const int c = code == -1 ? 2 : (code == -2 ? 1 : 0);  // _window_value (:95-98)
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) v[j].v[i] = col[c][i];
-      }
-    }
-    Vec<T, VEC> o;
-#pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      float acc = bias[i];
-      acc += product<T>(xs.v[i], wq[3][i]);  // self * w3, parent * w2, grandparent * w1, great-grandparent * w0
-      acc += product<T>(v[0].v[i], wq[2][i]);
-      acc += product<T>(v[1].v[i], wq[1][i]);
-      acc += product<T>(v[2].v[i], wq[0][i]);
-      if (a.silu) acc = acc / (1.0f + expf(-acc));
-      o.v[i] = T::from_f32(acc);
-    }
-    if (nvec == VEC) {
-      store_vec<T, VEC>(out + t * a.stride_o_token, a.stride_o_dim, oc, o);
+  // ---- stage: node inputs, ancestor codes, weights, bias, state ---------------------------------------------------
+  const bool xvec = a.stride_x_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                    ((a.stride_x_token | a.stride_x_seq | cb) & 7) == 0;
+  for (int i = tid; i < n * kVecs; i += kThreads) {
+    const int t = i / kVecs, v = i % kVecs;
+    const uint16_t* p = x + t * a.stride_x_token + 8 * v * a.stride_x_dim;
+    uint4 r;
+    if (xvec) {
+      r = *reinterpret_cast<const uint4*>(p);
     } else {
-      for (int i = 0; i < nvec; ++i) out[t * a.stride_o_token + i * a.stride_o_dim] = o.v[i];
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = 8 * v + e < nch ? p[e * a.stride_x_dim] : 0u;
+      r = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
     }
-    if (window != nullptr) {  // slot 0 grandparent, 1 parent, 2 self (:241-264)
-      S* wp = window + t * a.stride_win_step;
-      for (int i = 0; i < nvec; ++i) {
-        wp[i * a.stride_win_dim + 0 * a.stride_win_win] = v[1].v[i];
-        wp[i * a.stride_win_dim + 1 * a.stride_win_win] = v[0].v[i];
-        wp[i * a.stride_win_dim + 2 * a.stride_win_win] = xs.v[i];
+    xs[i] = r;
+  }
+  const int32_t* atab = a.ancestors + static_cast<int64_t>(seq) * 3 * a.seqlen;
+  for (int i = tid; i < 3 * n; i += kThreads) anc[i] = atab[(i / n) * a.seqlen + i % n];
+  {
+    const bool tap_fast = a.stride_w_width == 1;  // lanes along the weight's contiguous dimension
+    const uint16_t* wsrc = static_cast<const uint16_t*>(a.weight) + static_cast<int64_t>(cb) * a.stride_w_dim;
+    for (int i = tid; i < 4 * kChannels; i += kThreads) {
+      const int c = tap_fast ? i / 4 : i % kChannels, j = tap_fast ? i % 4 : i / kChannels;
+      wts[j * kChannels + c] = c < nch ? wsrc[c * a.stride_w_dim + j * a.stride_w_width] : 0;
+    }
+    for (int c = tid; c < kChannels; c += kThreads)
+      bias_s[c] = (c < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c, a.bias_dtype) : 0.f;
+  }
+  const bool tok_fast = a.stride_cs_tok == 1;  // lanes along the state's contiguous dimension
+  if (off.row_roll) {
+    const uint4* src = reinterpret_cast<const uint4*>(state);
+    uint4* dst = reinterpret_cast<uint4*>(rows);
+    for (int i = tid; i < kChannels * L / 8; i += kThreads) dst[i] = src[i];
+  } else {
+    for (int i = tid; i < 3 * kChannels; i += kThreads) {
+      const int c = tok_fast ? i / 3 : i % kChannels, j = tok_fast ? i % 3 : i / kChannels;
+      hist[j * kChannels + c] = c < nch ? state[c * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : 0;
+    }
+  }
+  __syncthreads();
+  if (off.row_roll) {  // the history columns out of the staged rows, before the roll rewrites them
+    for (int i = tid; i < 3 * kChannels; i += kThreads) {
+      const int c = i / 3, j = i % 3;
+      hist[j * kChannels + c] = rows[c * L + history + j];
+    }
+    __syncthreads();
+  }
+
+  // ---- outputs: thread (token lane tl, vector v) computes channels 8 v .. 8 v + 7 of nodes tl, tl + kTokLanes, ... ---
+  {
+    const int v = tid % kVecs, tl = tid / kVecs;
+    const int c0 = 8 * v;
+    const bool ovec = a.stride_o_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+                      ((a.stride_o_token | a.stride_o_seq | cb) & 7) == 0;
+    uint16_t* window = nullptr;
+    if (a.window != nullptr)
+      window = static_cast<uint16_t*>(a.window) + e4::ld(a.window_indices, seq) * a.stride_win_seq +
+               static_cast<int64_t>(cb + c0) * a.stride_win_dim;
+    uint4 wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv[j] = *reinterpret_cast<const uint4*>(&wts[j * kChannels + c0]);
+    const float4 b0 = *reinterpret_cast<const float4*>(&bias_s[c0]), b1 = *reinterpret_cast<const float4*>(&bias_s[c0 + 4]);
+    const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    for (int t = tl; t < n; t += kTokLanes) {
+      const uint4 xt = xs[t * kVecs + v];
+      uint4 win[3];  // parent, grandparent, great-grandparent
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int code = anc[j * n + t];
+        // _window_value (:95-98): history column 2 (code -1), 1 (-2), 0 (-3)
+        win[j] = code >= 0 ? xs[code * kVecs + v] : *reinterpret_cast<const uint4*>(&hist[(code + 3) * kChannels + c0]);
+      }
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float r[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          float acc = bias[e + k];
+          // self w3, parent w2, grandparent w1, great-grandparent w0
+          acc += product<T>(lane16(xt, e + k), lane16(wv[3], e + k));
+          acc += product<T>(lane16(win[0], e + k), lane16(wv[2], e + k));
+          acc += product<T>(lane16(win[1], e + k), lane16(wv[1], e + k));
+          acc += product<T>(lane16(win[2], e + k), lane16(wv[0], e + k));
+          if (a.silu) acc = silu(acc);
+          r[k] = acc;
+        }
+        o[e / 2] = static_cast<uint32_t>(T::from_f32(r[0])) | static_cast<uint32_t>(T::from_f32(r[1])) << 16;
+      }
+      uint16_t* op = out + t * a.stride_o_token + c0 * a.stride_o_dim;
+      if (ovec) {
+        *reinterpret_cast<uint4*>(op) = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (c0 + e < nch) op[e * a.stride_o_dim] = static_cast<uint16_t>((e & 1) ? o[e / 2] >> 16 : o[e / 2] & 0xffffu);
+      }
+      if (window != nullptr) {  // slot 0 grandparent, 1 parent, 2 self (:241-264)
+        uint16_t* wp = window + t * a.stride_win_step;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (c0 + e >= nch) break;
+          wp[e * a.stride_win_dim + 0 * a.stride_win_win] = lane16(win[1], e);
+          wp[e * a.stride_win_dim + 1 * a.stride_win_win] = lane16(win[0], e);
+          wp[e * a.stride_win_dim + 2 * a.stride_win_win] = lane16(xt, e);
+        }
       }
     }
-    // the roll (:266-278): input t goes to column t + 3 + shift; every history read is already done
-    const int64_t dest = t + 3 + shift;
-    if (dest >= 0)
-      for (int i = 0; i < nvec; ++i) state[i * a.stride_cs_dim + dest * a.stride_cs_tok] = xs.v[i];
   }
+
+  // ---- the roll (:266-278): history column j goes to column j + shift, node t's input to t + 3 + shift (kept when
+  // the column is >= 0); every history read was staged before the first barrier -----------------------------------
+  const int shift = static_cast<int>((num_tokens + 2 < L ? num_tokens + 2 : L) - num_tokens - 3);
+  const int cols = 3 + n;  // source columns: history 0..2, then the nodes
+  if (off.row_roll) {
+    // the block's rows assembled 8 elements at a time: column col of channel c takes source col - shift when that is
+    // a source column, and keeps its staged value otherwise
+    const uint4* old = reinterpret_cast<const uint4*>(rows);
+    uint4* dst = reinterpret_cast<uint4*>(state);
+    for (int i = tid; i < kChannels * L / 8; i += kThreads) {
+      int c = (8 * i) / L, col = 8 * i - c * L;
+      const uint4 o = old[i];
+      uint32_t w[4];
 #pragma unroll
-  for (int j = 0; j < 3; ++j) {
-    const int64_t dest = j + shift;
-    if (dest >= 0)
-      for (int i = 0; i < nvec; ++i) state[i * a.stride_cs_dim + dest * a.stride_cs_tok] = col[j][i];
+      for (int e = 0; e < 8; ++e) {
+        const int src = col - shift;
+        uint16_t val = lane16(o, e);
+        if (src >= 0 && src < cols)
+          val = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
+        w[e / 2] = (e & 1) ? (w[e / 2] | static_cast<uint32_t>(val) << 16) : val;
+        if (++col == L) {
+          col = 0;
+          ++c;
+        }
+      }
+      dst[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  } else {
+    for (int i = tid; i < cols * kChannels; i += kThreads) {
+      const int c = tok_fast ? i / cols : i % kChannels, src = tok_fast ? i % cols : i / kChannels;
+      const int64_t dest = src + shift;
+      if (c >= nch || dest < 0) continue;
+      const uint16_t val = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
+      state[c * a.stride_cs_dim + dest * a.stride_cs_tok] = val;
+    }
   }
 }
 
@@ -161,15 +255,15 @@ __global__ __launch_bounds__(256) void tree_conv_kernel(const eagle4_conv_args a
 extern "C" int eagle4_gdn_tree_conv1d_update(const eagle4_conv_args* a, void* stream) {
   if (a->batch == 0 || a->dim == 0) return EAGLE4_OK;
   if ((a->dtype != EAGLE4_BF16 && a->dtype != EAGLE4_F16) || a->state_len < 3 || a->seqlen < 1 ||
-      a->conv_state_indices.ptr == nullptr || a->ancestors == nullptr ||
+      a->seqlen > kMaxNodes || a->conv_state_indices.ptr == nullptr || a->ancestors == nullptr ||
       (a->window != nullptr && a->window_indices.ptr == nullptr))
     return EAGLE4_NOT_COVERED;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  constexpr int kVec = 8;
-  const dim3 grid(e4::ceil_div(e4::ceil_div(a->dim, kVec), 256), a->batch);
+  const Lds off = lds_layout(*a);
+  const dim3 grid(e4::ceil_div(a->dim, kChannels), a->batch);
   if (a->dtype == EAGLE4_BF16)
-    tree_conv_kernel<e4::Bf16, kVec><<<grid, 256, 0, s>>>(*a);
+    tree_conv_kernel<e4::Bf16><<<grid, kThreads, off.total, s>>>(*a, off);
   else
-    tree_conv_kernel<e4::F16, kVec><<<grid, 256, 0, s>>>(*a);
+    tree_conv_kernel<e4::F16><<<grid, kThreads, off.total, s>>>(*a, off);
   return E4_LAUNCH_STATUS();
 }
