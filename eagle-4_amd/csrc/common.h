@@ -99,18 +99,35 @@ E4_DEV void st(const eagle4_itab& t, int64_t i, int64_t j, int64_t v) {
 }
 
 // ---- lane reductions (wave64) -----------------------------------------------------------------------------------------
-// Butterfly sum over groups of C adjacent lanes (C a power of two <= 64); every lane of a group gets the group sum.
+// A value of another lane of the same row of 16, through a DPP lane pattern (one VALU operand modifier, no LDS trip).
+template <int kCtrl>
+E4_DEV float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xF, 0xF, true));
+}
+
+// Sum over groups of C adjacent lanes (C a power of two <= 64, all lanes active); every lane of a group gets the same
+// bits. Within a row of 16 the partner lanes come by DPP: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
+// (lane ^ 2), row_half_mirror (the other quad of an 8) and row_mirror (the other 8 of the 16); wider groups use
+// ds_bpermute shuffles.
 template <int C>
 E4_DEV float group_sum(float x) {
-#pragma unroll
-  for (int m = 1; m < C; m <<= 1) x += __shfl_xor(x, m, 64);
+  if constexpr (C >= 2) x += dpp<0xB1>(x);
+  if constexpr (C >= 4) x += dpp<0x4E>(x);
+  if constexpr (C >= 8) x += dpp<0x141>(x);
+  if constexpr (C >= 16) x += dpp<0x140>(x);
+  if constexpr (C >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (C >= 64) x += __shfl_xor(x, 32, 64);
   return x;
 }
 
 template <int C>
 E4_DEV float group_max(float x) {
-#pragma unroll
-  for (int m = 1; m < C; m <<= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  if constexpr (C >= 2) x = fmaxf(x, dpp<0xB1>(x));
+  if constexpr (C >= 4) x = fmaxf(x, dpp<0x4E>(x));
+  if constexpr (C >= 8) x = fmaxf(x, dpp<0x141>(x));
+  if constexpr (C >= 16) x = fmaxf(x, dpp<0x140>(x));
+  if constexpr (C >= 32) x = fmaxf(x, __shfl_xor(x, 16, 64));
+  if constexpr (C >= 64) x = fmaxf(x, __shfl_xor(x, 32, 64));
   return x;
 }
 

@@ -1,19 +1,32 @@
 // Gated delta rule over a draft tree on gfx950, snapshot contract (kernels/gdn_tree_recurrence.py:204-359, 562-706).
 //
-// Roofline: HBM writes. Every node of every (request, value head) writes its whole fp32 [V, K] state (64 KB at
-// V = K = 128) and reads ~1 KB of inputs, at ~1.7 FLOP per byte. The layout is chosen for the stores:
+// Roofline: HBM writes. Every node of every (request, value head) writes its whole [V, K] state snapshot (64 KB in
+// fp32 at V = K = 128) and reads ~1 KB of inputs, at ~1.7 FLOP per byte. The layout is chosen for the stores:
 //
-//  * A workgroup owns one (V tile, request, value head) and walks the request's nodes in order; the state tile lives
-//    in VGPRs for the whole walk.
-//  * C adjacent lanes share a V row, each holding E = K / C state values as E/4 float4 chunks at
-//    k = 4c + 4Cj (c = lane % C, j = chunk). At K = 128, C = 8: one store instruction of a wave writes 8 rows x 128
-//    contiguous bytes -> every snapshot store is full 128-byte lines, streamed once.
-//  * The K reductions (h k and h q) are C-lane butterflies; q / k norms reduce the same way. No LDS is used.
-//  * A chain child of an fp32 state continues from the registers (bitwise what a reload gives); any other node
-//    reloads its parent's snapshot, which the same thread wrote (same addresses, same lane), so no barrier is needed.
+//  * A workgroup is one wave and owns one (V tile, request, value head); the tile's state lives in VGPRs for the
+//    whole walk.
+//  * C adjacent lanes share a V row, each holding E = K / C state values as E/4 float4 chunks at k = 4c + 4Cj
+//    (c = lane % C, j = chunk). At K = 128, C = 8: one store instruction writes 8 rows x 128 contiguous bytes, so
+//    every snapshot store is whole 128-byte lines, streamed once.
+//  * The K reductions (h k and h q) are C-lane butterflies; q / k norms reduce the same way.
+//
+// Which state a node starts from. The reference walks the rows in index order and, for every node but the root,
+// reloads its parent's snapshot from the buffer it has just written (an fp32 chain child, parent = previous row,
+// continues from registers instead; :318-329). Rows are parent first but otherwise in any order, so in index order
+// most parents are not the row just computed and ~3/4 of the nodes reload 64 KB each. Here a request whose reloads
+// are guaranteed to return the parent's own snapshot (parents precede children, every row has a real slot, no two
+// rows share one, at most 64 rows) is walked depth first instead (pre-order, children by index): a node's first
+// child continues from the registers, and a node with more children parks its state on a small per-wave LDS stack
+// that its later children pop (LIFO: when a later child of p comes, every state pushed after p has been popped).
+// Parked states are what a reload would give (rounded through the snapshot dtype; exact in fp32), so the results
+// are bit-identical to the index-order walk. When the stack is full a node is not parked and its later children
+// reload its snapshot from HBM, as the reference does. Any other request keeps the reference's index-order walk
+// with its reloads (the same wave wrote the snapshot it reads: same addresses, same lane, so no barrier is needed).
 //
 // The math and its order follow the walk: h *= exp(g); v' = (v - h k) * beta; h += k v'; o = h q, with beta
 // rounded through b's dtype and q, k L2-normalised with 1e-6 inside the square root.
+
+#include <type_traits>
 
 #include "common.h"
 
@@ -58,64 +71,132 @@ E4_DEV void load4_code(const void* base, int64_t off, int dtype, float* out) {
     load4<e4::F16>(static_cast<const uint16_t*>(base) + off, out);
 }
 
-// Per-node inputs of one lane: its E values of q and k, and v of its RPT rows.
-template <int E, int RPT>
-struct NodeIn {
-  float q[E], k[E], v[RPT];
-  float a, b;
-  int32_t parent;
-};
+// Four raw input values (q or k) as loaded: a float4 for fp32 inputs, four 16-bit values in a uint2 otherwise.
+template <typename T>
+using Raw4 = typename std::conditional<sizeof(typename T::storage) == 4, float4, uint2>::type;
 
-template <int K, int C, int RPT, typename Tin>
-E4_DEV void load_node(NodeIn<K / C, RPT>& in, const eagle4_gdn_args& a, int64_t t, int n, int step, int ih, int hv,
-                      int c, const int* rows, bool valid) {
-  constexpr int E = K / C;
-  using S = typename Tin::storage;
-  if (!valid) return;
-  const S* q = static_cast<const S*>(a.q) + t * a.stride_q + static_cast<int64_t>(ih) * K;
-  const S* k = static_cast<const S*>(a.k) + t * a.stride_k + static_cast<int64_t>(ih) * K;
-#pragma unroll
-  for (int j = 0; j < E / 4; ++j) {
-    load4<Tin>(q + 4 * c + 4 * C * j, &in.q[4 * j]);
-    load4<Tin>(k + 4 * c + 4 * C * j, &in.k[4 * j]);
+template <typename T>
+E4_DEV void widen4(const Raw4<T>& r, float* out) {
+  if constexpr (sizeof(typename T::storage) == 4) {
+    out[0] = r.x;
+    out[1] = r.y;
+    out[2] = r.z;
+    out[3] = r.w;
+  } else {
+    out[0] = T::to_f32(static_cast<uint16_t>(r.x & 0xffffu));
+    out[1] = T::to_f32(static_cast<uint16_t>(r.x >> 16));
+    out[2] = T::to_f32(static_cast<uint16_t>(r.y & 0xffffu));
+    out[3] = T::to_f32(static_cast<uint16_t>(r.y >> 16));
   }
-  const S* v = static_cast<const S*>(a.v) + t * a.stride_v + static_cast<int64_t>(hv) * a.V;
-#pragma unroll
-  for (int s = 0; s < RPT; ++s) in.v[s] = rows[s] < a.V ? Tin::to_f32(v[rows[s]]) : 0.f;
-  in.a = e4::load_scalar(a.a, t * a.stride_a + hv, a.gate_dtype);
-  in.b = e4::load_scalar(a.b, t * a.stride_b + hv, a.gate_dtype);
-  in.parent = static_cast<int32_t>(e4::ld(a.parents, n, step));
 }
 
-// One workgroup: 4 waves; rows of the V tile: RPT slots x 4 waves x (64 / C) rows.
-template <int K, int C, int RPT, typename Tin, typename Tsnap>
-__global__ __launch_bounds__(256) void gdn_tree_walk_kernel(const eagle4_gdn_args a) {
+// A gate value of a runtime dtype, as raw bits (loaded here, widened where it is used: a conversion next to its load
+// would make the compiler wait for every store in flight too, since vmcnt counts stores).
+E4_DEV uint32_t load_raw(const void* p, int64_t i, int dtype) {
+  if (dtype == EAGLE4_F32) return static_cast<const uint32_t*>(p)[i];
+  return static_cast<const uint16_t*>(p)[i];
+}
+
+E4_DEV float widen_raw(uint32_t r, int dtype) {
+  if (dtype == EAGLE4_F32) return __uint_as_float(r);
+  if (dtype == EAGLE4_BF16) return e4::bf16_to_f32(static_cast<uint16_t>(r));
+  return e4::f16_to_f32(static_cast<uint16_t>(r));
+}
+
+// The gate of a node (:115-140): the decay exp(g) and the write strength beta (rounded through b's dtype).
+E4_DEV float2 gate_of(uint32_t a_raw, uint32_t b_raw, const eagle4_gdn_args& a, float A, float dt_bias) {
+  const float x = widen_raw(a_raw, a.gate_dtype) + dt_bias;
+  const float bx = a.softplus_beta * x;
+  const float softplus = bx <= a.softplus_threshold ? (1.0f / a.softplus_beta) * logf(1.0f + expf(bx)) : x;
+  const float decay = expf(A * softplus);
+  const float beta = e4::round_code(1.0f / (1.0f + expf(-widen_raw(b_raw, a.gate_dtype))), a.gate_dtype);
+  return make_float2(decay, beta);
+}
+
+// Waits for every vector memory operation of the wave (vmcnt(0); expcnt and lgkmcnt untouched). Placed right after a
+// load on a rarely taken path, it settles the loaded registers there, so the compiler does not wait for them (and with
+// them for every store in flight) where that path joins the main one.
+E4_DEV void settle_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+E4_DEV int readlane(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
+E4_DEV uint64_t readlane64(uint64_t x, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(x & 0xffffffffu), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(x >> 32), l);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One node's inputs in a lane's registers: its E values of q and k (raw), v of its RPT rows (raw), and the node's
+// scalars (decay, beta, qs = scale / |q|, ks = 1 / |k|).
+template <int E, int RPT, typename Tin>
+struct Node {
+  Raw4<Tin> q[E / 4], k[E / 4];
+  typename Tin::storage v[RPT];
+  float4 sc;
+};
+
+// Workgroup: WAVES waves over consecutive V rows of one (request, value head); each wave owns RPT x (64 / C) rows.
+// The request's first TS nodes are staged in LDS up front (q, k, the workgroup's v rows, and the node scalars), so the
+// walk itself issues no global loads for them: a vector load in the walk would wait for the snapshot stores before it
+// (loads and stores share the vmcnt counter), which serialises the walk on the store latency.
+template <int K, int C, int RPT, int WAVES, int S, typename Tin, typename Tsnap>
+__global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_gdn_args a) {
   constexpr int E = K / C;
   constexpr int NJ = E / 4;
-  constexpr int ROWS_WAVE = 64 / C;
-  constexpr int ROWS_WG = RPT * 4 * ROWS_WAVE;
+  constexpr int ROWS_WAVE = RPT * (64 / C);
+  constexpr int ROWS = WAVES * ROWS_WAVE;
+  constexpr int NT = 64 * WAVES;
   static_assert(E % 4 == 0 && C <= 64, "lane layout");
+  using IS = typename Tin::storage;
   using SS = typename Tsnap::storage;
+  constexpr int TS = sizeof(IS) == 4 ? 8 : 16;  // staged nodes
+  constexpr bool kExact = sizeof(SS) == 4;      // fp32 snapshots: a reload gives the registers bit for bit
+  __shared__ float4 stack[WAVES][S][RPT * NJ][64];
+  __shared__ __align__(16) IS s_q[TS][K];
+  __shared__ __align__(16) IS s_k[TS][K];
+  __shared__ IS s_v[TS][ROWS];
+  __shared__ float4 s_sc[TS];
 
+#ifdef E4_GDN_N_FAST
   const int n = blockIdx.y, hv = blockIdx.z;
+#else
+  const int n = blockIdx.z, hv = blockIdx.y;
+#endif
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane % C, rr = lane / C;
   const int ih = hv / (a.HV / a.H);
-  int rows[RPT];
+  const int row0 = blockIdx.x * ROWS;
+  int rows[RPT], lrow[RPT];
 #pragma unroll
-  for (int s = 0; s < RPT; ++s) rows[s] = blockIdx.x * ROWS_WG + s * 4 * ROWS_WAVE + wave * ROWS_WAVE + rr;
+  for (int s = 0; s < RPT; ++s) {
+    lrow[s] = wave * ROWS_WAVE + s * (64 / C) + rr;
+    rows[s] = row0 + lrow[s];
+  }
 
   if (a.publish != nullptr && blockIdx.x == 0 && hv == 0) {  // _publish_slot_table (:188-200)
-    for (int i = tid; i < a.num_slot_cols; i += blockDim.x)
+    for (int i = tid; i < a.num_slot_cols; i += NT)
       a.publish[n * a.stride_publish + i] = static_cast<int32_t>(e4::ld(a.snap_indices, n, i));
   }
   const int64_t bos = e4::ld(a.cu_seqlens, n);
   const int T = static_cast<int>(e4::ld(a.cu_seqlens, n + 1) - bos);
+  if (T <= 0) return;
+  const int64_t cache_idx = e4::ld(a.snap_indices, n, 0);  // the request's scratch row (per-row slots: row 0's slot)
+  const float A = -expf(e4::load_scalar(a.A_log, hv, a.A_log_dtype));
+  const float dt_bias = e4::load_scalar(a.dt_bias, hv, a.dt_bias_dtype);
 
+  // The walk plan: lane i holds row i's parent, slot and children (a bit mask). Depth first needs reloads that
+  // return the parent's own snapshot.
+  int par = 0;
+  int64_t my_slot = cache_idx;
+  uint64_t kids = 0;
+  bool dfs = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
+  if (dfs && lane < T) {
+    par = static_cast<int>(e4::ld(a.parents, n, lane));
+    if (a.row_slots) my_slot = e4::ld(a.snap_indices, n, lane);
+  }
   // the initial state (:284-296); with num_accepted its slot is in column num_accepted - 1
   float h[RPT][E];
-  int64_t idx = a.num_accepted.ptr != nullptr ? e4::ld(a.h0_indices, n, e4::ld(a.num_accepted, n) - 1)
-                                              : e4::ld(a.h0_indices, n, 0);
+  const int64_t idx = a.num_accepted.ptr != nullptr ? e4::ld(a.h0_indices, n, e4::ld(a.num_accepted, n) - 1)
+                                                    : e4::ld(a.h0_indices, n, 0);
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
 #pragma unroll
   for (int s = 0; s < RPT; ++s) {
@@ -126,116 +207,295 @@ __global__ __launch_bounds__(256) void gdn_tree_walk_kernel(const eagle4_gdn_arg
                    a.h0_dtype, &h[s][4 * j]);
       } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[s][4 * j + e] = 0.f;
+        for (int e = 0; e < 4; ++e) h[s][e + 4 * j] = 0.f;
       }
     }
   }
-  const int64_t cache_idx = e4::ld(a.snap_indices, n, 0);  // the request's scratch row (per-row slots: row 0's slot)
-  const float A = -expf(e4::load_scalar(a.A_log, hv, a.A_log_dtype));
-  const float dt_bias = e4::load_scalar(a.dt_bias, hv, a.dt_bias_dtype);
+  // ---- staging: q, k, v and the node scalars of nodes [0, min(T, TS)) --------------------------------------------
+  const int ts = T < TS ? T : TS;
+  {
+    constexpr int CH = K / 4;  // Raw4 chunks per q / k row
+    for (int i = tid; i < ts * CH; i += NT) {
+      const int t = i / CH, ch = i % CH;
+      const int64_t tok = bos + t;
+      *reinterpret_cast<Raw4<Tin>*>(&s_q[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
+          static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K + 4 * ch);
+      *reinterpret_cast<Raw4<Tin>*>(&s_k[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
+          static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K + 4 * ch);
+    }
+    for (int i = tid; i < ts * ROWS; i += NT) {
+      const int t = i / ROWS, r = i % ROWS;
+      const int row = row0 + r < a.V ? row0 + r : a.V - 1;  // rows past V are computed and dropped
+      s_v[t][r] = static_cast<const IS*>(a.v)[(bos + t) * a.stride_v + static_cast<int64_t>(hv) * a.V + row];
+    }
+    if (tid < ts) {
+      const float2 g = gate_of(load_raw(a.a, (bos + tid) * a.stride_a + hv, a.gate_dtype),
+                               load_raw(a.b, (bos + tid) * a.stride_b + hv, a.gate_dtype), a, A, dt_bias);
+      s_sc[tid] = make_float4(g.x, g.y, 0.f, 0.f);
+    }
+  }
+  __syncthreads();
+  for (int t = wave; t < ts; t += WAVES) {  // L2 norms over K (:143-151), one node per wave
+    float qq = 0.f, kk = 0.f;
+    for (int e = lane; e < K; e += 64) {
+      const float qv = Tin::to_f32(s_q[t][e]), kv = Tin::to_f32(s_k[t][e]);
+      qq = fmaf(qv, qv, qq);
+      kk = fmaf(kv, kv, kk);
+    }
+    qq = e4::group_sum<64>(qq);
+    kk = e4::group_sum<64>(kk);
+    if (lane == 0) {
+      s_sc[t].z = a.scale / sqrtf(qq + 1e-6f);
+      s_sc[t].w = 1.0f / sqrtf(kk + 1e-6f);
+    }
+  }
+  __syncthreads();
+
+  if (dfs) {
+    bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot <= a.pad_slot_id);
+    if (a.row_slots) {
+      for (int j = 0; j < T; ++j) {
+        const uint64_t sj = readlane64(static_cast<uint64_t>(my_slot), j);
+        bad = bad || (lane < T && lane != j && static_cast<uint64_t>(my_slot) == sj);
+      }
+    }
+    dfs = __ballot(bad) == 0;
+    if (dfs) {
+      for (int i = 0; i + 1 < T; ++i) {
+        const uint64_t m = __ballot(lane > 0 && lane < T && par == i);
+        if (lane == i) kids = m;
+      }
+    }
+  }
+
+  settle_loads();  // the initial state and the plan tables
+  // A node's inputs: staged ones from LDS, later ones (T > TS) from global memory with their scalars computed here.
+  auto fetch = [&](Node<E, RPT, Tin>& nd, int u) {
+    if (u < TS) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        nd.q[j] = *reinterpret_cast<const Raw4<Tin>*>(&s_q[u][4 * c + 4 * C * j]);
+        nd.k[j] = *reinterpret_cast<const Raw4<Tin>*>(&s_k[u][4 * c + 4 * C * j]);
+      }
+#pragma unroll
+      for (int s = 0; s < RPT; ++s) nd.v[s] = s_v[u][lrow[s]];
+      nd.sc = s_sc[u];
+    } else {
+      const int64_t tok = bos + u;
+      const IS* q = static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K;
+      const IS* k = static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K;
+      float qq = 0.f, kk = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        nd.q[j] = *reinterpret_cast<const Raw4<Tin>*>(q + 4 * c + 4 * C * j);
+        nd.k[j] = *reinterpret_cast<const Raw4<Tin>*>(k + 4 * c + 4 * C * j);
+        float qf[4], kf[4];
+        widen4<Tin>(nd.q[j], qf);
+        widen4<Tin>(nd.k[j], kf);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qq = fmaf(qf[e], qf[e], qq);
+          kk = fmaf(kf[e], kf[e], kk);
+        }
+      }
+      qq = e4::group_sum<C>(qq);
+      kk = e4::group_sum<C>(kk);
+      const IS* v = static_cast<const IS*>(a.v) + tok * a.stride_v + static_cast<int64_t>(hv) * a.V;
+#pragma unroll
+      for (int s = 0; s < RPT; ++s) nd.v[s] = v[rows[s] < a.V ? rows[s] : a.V - 1];
+      const float2 g = gate_of(load_raw(a.a, tok * a.stride_a + hv, a.gate_dtype),
+                               load_raw(a.b, tok * a.stride_b + hv, a.gate_dtype), a, A, dt_bias);
+      nd.sc = make_float4(g.x, g.y, a.scale / sqrtf(qq + 1e-6f), 1.0f / sqrtf(kk + 1e-6f));
+      settle_loads();
+    }
+  };
+
   SS* snap = static_cast<SS*>(a.snap);
 
-  NodeIn<E, RPT> cur, nxt;
-  load_node<K, C, RPT, Tin>(cur, a, bos, n, 0, ih, hv, c, rows, T > 0);
-  for (int step = 0; step < T; ++step) {
-    const int parent = cur.parent;
-    load_node<K, C, RPT, Tin>(nxt, a, bos + step + 1, n, step + 1, ih, hv, c, rows, step + 1 < T);
-    int64_t slot = cache_idx, parent_slot = cache_idx;
-    if (a.row_slots) {
-      slot = e4::ld(a.snap_indices, n, step);
-      parent_slot = step != 0 ? e4::ld(a.snap_indices, n, parent) : a.pad_slot_id;  // the root reads nothing
-    }
-    bool reload = step != 0 && parent_slot > a.pad_slot_id;  // :318-329
-    if (a.skip_chain_reload) reload = reload && parent != step - 1;
-    if (reload) {
-      const SS* src = snap + parent_slot * a.stride_snap_slot + static_cast<int64_t>(parent) * a.stride_snap_row + head_off;
+  // a node's snapshot in the buffer (slot, row)
+  auto snap_at = [&](int64_t slot_of, int row) {
+    return snap + slot_of * a.stride_snap_slot + static_cast<int64_t>(row) * a.stride_snap_row + head_off;
+  };
+  auto reload = [&](const SS* src) {
 #pragma unroll
-      for (int s = 0; s < RPT; ++s)
+    for (int s = 0; s < RPT; ++s)
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-          if (rows[s] < a.V) load4<Tsnap>(src + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+      for (int j = 0; j < NJ; ++j)
+        if (rows[s] < a.V) load4<Tsnap>(src + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+    settle_loads();
+  };
+  float4 (*const my_stack)[RPT * NJ][64] = stack[wave];
+
+  Node<E, RPT, Tin> cur, nxt;
+  fetch(cur, 0);
+  int u = 0, sp = 0;
+  uint64_t unparked = 0;  // nodes with several children that found the stack full
+  for (int it = 0; it < T; ++it) {
+    // the next node and where its state comes from
+    int next = -1;
+    bool next_first = false, next_last = false;
+    if (dfs) {
+      const uint64_t ku = readlane64(kids, u);
+      if (ku != 0) {
+        next = __builtin_ctzll(ku);
+        next_first = true;
+      } else {
+        for (int x = u; x != 0;) {
+          const int px = readlane(par, x);
+          const uint64_t sib = x == 63 ? 0 : readlane64(kids, px) & (~0ull << (x + 1));
+          if (sib != 0) {
+            next = __builtin_ctzll(sib);
+            next_last = (sib & (sib - 1)) == 0;
+            break;
+          }
+          x = px;
+        }
+      }
+    } else if (u + 1 < T) {
+      next = u + 1;
     }
-    // gate and write strength (:115-140)
-    const float x = cur.a + dt_bias;
-    const float bx = a.softplus_beta * x;
-    const float softplus = bx <= a.softplus_threshold ? (1.0f / a.softplus_beta) * logf(1.0f + expf(bx)) : x;
-    const float decay = expf(A * softplus);
-    const float beta = e4::round_code(1.0f / (1.0f + expf(-cur.b)), a.gate_dtype);
-    // L2 norms over K (:143-151)
-    float qq = 0.f, kk = 0.f;
+    if (next >= 0 && next < TS) fetch(nxt, next);  // staged: LDS reads only, ahead of their use
+
+    // the delta rule step (:167-185) with the normalisation folded into the dot products and the update:
+    // h k^ = ks (h k), k^ dv = k (ks dv), o = qs (h q)
+    const float decay = cur.sc.x, beta = cur.sc.y, qs = cur.sc.z, ks = cur.sc.w;
+    const float dks = decay * ks;
+    float qf[E], kf[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      qq = fmaf(cur.q[e], cur.q[e], qq);
-      kk = fmaf(cur.k[e], cur.k[e], kk);
+    for (int j = 0; j < NJ; ++j) {
+      widen4<Tin>(cur.q[j], &qf[4 * j]);
+      widen4<Tin>(cur.k[j], &kf[4 * j]);
     }
-    qq = e4::group_sum<C>(qq);
-    kk = e4::group_sum<C>(kk);
-    const float qinv = 1.0f / sqrtf(qq + 1e-6f);
-    const float kinv = 1.0f / sqrtf(kk + 1e-6f);
-    float qn[E], kn[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      qn[e] = (cur.q[e] * qinv) * a.scale;
-      kn[e] = cur.k[e] * kinv;
-    }
-    // the delta rule step (:167-185)
     float o[RPT];
 #pragma unroll
     for (int s = 0; s < RPT; ++s) {
       float hk = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        h[s][e] *= decay;
-        hk = fmaf(h[s][e], kn[e], hk);
-      }
+      for (int e = 0; e < E; ++e) hk = fmaf(h[s][e], kf[e], hk);
       hk = e4::group_sum<C>(hk);
-      const float dv = (cur.v[s] - hk) * beta;
+      const float kdv = (Tin::to_f32(cur.v[s]) - hk * dks) * beta * ks;
       float hq = 0.f;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        h[s][e] = fmaf(kn[e], dv, h[s][e]);
-        hq = fmaf(h[s][e], qn[e], hq);
+        h[s][e] = fmaf(kf[e], kdv, h[s][e] * decay);
+        hq = fmaf(h[s][e], qf[e], hq);
       }
-      o[s] = e4::group_sum<C>(hq);
+      o[s] = e4::group_sum<C>(hq) * qs;
     }
-    const int64_t t = bos + step;
+    const int64_t t = bos + u;
     if (c == 0) {
 #pragma unroll
       for (int s = 0; s < RPT; ++s)
         if (rows[s] < a.V) e4::store_scalar(a.out, t * a.stride_o + static_cast<int64_t>(hv) * a.V + rows[s], a.out_dtype, o[s]);
     }
+    int64_t slot = cache_idx;
+    if (a.row_slots) {
+      if (dfs) {
+        slot = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), u));
+      } else {
+        slot = e4::ld(a.snap_indices, n, u);
+        settle_loads();
+      }
+    }
     if (slot > a.pad_slot_id) {
-      SS* dst = snap + slot * a.stride_snap_slot + static_cast<int64_t>(step) * a.stride_snap_row + head_off;
+      SS* dst = snap_at(slot, u);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
 #pragma unroll
         for (int s = 0; s < RPT; ++s)
           if (rows[s] < a.V) store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
     }
-    cur = nxt;
+
+    // the state the next node starts from
+    if (next >= 0) {
+      if (dfs) {
+        const uint64_t ku = readlane64(kids, u);
+        if ((ku & (ku - 1)) != 0) {  // several children: park the state (as a reload would give it) for the later ones
+          if (sp < S) {
+#pragma unroll
+            for (int s = 0; s < RPT; ++s)
+#pragma unroll
+              for (int j = 0; j < NJ; ++j) {
+                float4 w = make_float4(h[s][4 * j], h[s][4 * j + 1], h[s][4 * j + 2], h[s][4 * j + 3]);
+                if constexpr (!kExact)
+                  w = make_float4(e4::round_through<Tsnap>(w.x), e4::round_through<Tsnap>(w.y),
+                                  e4::round_through<Tsnap>(w.z), e4::round_through<Tsnap>(w.w));
+                my_stack[sp][s * NJ + j][lane] = w;
+              }
+            ++sp;
+          } else {
+            unparked |= 1ull << u;
+          }
+        }
+        if (next_first) {
+          if constexpr (!kExact) {
+            if (!(a.skip_chain_reload && next == u + 1)) {  // an fp32 chain child keeps the registers
+#pragma unroll
+              for (int s = 0; s < RPT; ++s)
+#pragma unroll
+                for (int e = 0; e < E; ++e) h[s][e] = e4::round_through<Tsnap>(h[s][e]);
+            }
+          }
+        } else {
+          const int p = readlane(par, next);
+          if ((unparked >> p) & 1) {
+            const int64_t pslot = a.row_slots ? static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), p)) : cache_idx;
+            reload(snap_at(pslot, p));
+          } else {
+#pragma unroll
+            for (int s = 0; s < RPT; ++s)
+#pragma unroll
+              for (int j = 0; j < NJ; ++j) {
+                const float4 w = my_stack[sp - 1][s * NJ + j][lane];
+                h[s][4 * j] = w.x;
+                h[s][4 * j + 1] = w.y;
+                h[s][4 * j + 2] = w.z;
+                h[s][4 * j + 3] = w.w;
+              }
+            if (next_last) --sp;
+          }
+        }
+      } else {
+        // the reference's rule (:312-329)
+        const int p = static_cast<int>(e4::ld(a.parents, n, next));
+        const int64_t pslot = a.row_slots && p >= 0 ? e4::ld(a.snap_indices, n, p) : cache_idx;
+        bool re = p >= 0 && pslot > a.pad_slot_id;
+        if (a.skip_chain_reload) re = re && p != next - 1;
+        if (re) reload(snap_at(pslot, p));
+      }
+      if (next < TS)
+        cur = nxt;
+      else
+        fetch(cur, next);
+    }
+    u = next;
   }
 }
 
-template <int K, int C, int RPT, typename Tin>
+template <int K, int C, int RPT, int WAVES, int S, typename Tin>
 int launch_snap(const eagle4_gdn_args& a, hipStream_t s) {
-  constexpr int ROWS_WG = RPT * 4 * (64 / C);
-  const dim3 grid(e4::ceil_div(a.V, ROWS_WG), a.N, a.HV);
+  constexpr int ROWS = WAVES * RPT * (64 / C);
+#ifdef E4_GDN_N_FAST
+  const dim3 grid(e4::ceil_div(a.V, ROWS), a.N, a.HV);
+#else
+  const dim3 grid(e4::ceil_div(a.V, ROWS), a.HV, a.N);
+#endif
   if (a.snap_dtype == EAGLE4_F32)
-    gdn_tree_walk_kernel<K, C, RPT, Tin, e4::F32><<<grid, 256, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_BF16)
-    gdn_tree_walk_kernel<K, C, RPT, Tin, e4::Bf16><<<grid, 256, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_F16)
-    gdn_tree_walk_kernel<K, C, RPT, Tin, e4::F16><<<grid, 256, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
   else
     return EAGLE4_NOT_COVERED;
   return E4_LAUNCH_STATUS();
 }
 
-template <int K, int C, int RPT>
+template <int K, int C, int RPT, int WAVES, int S>
 int launch_in(const eagle4_gdn_args& a, hipStream_t s) {
-  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, e4::Bf16>(a, s);
-  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, e4::F16>(a, s);
-  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, e4::F32>(a, s);
+  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, WAVES, S, e4::Bf16>(a, s);
+  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, WAVES, S, e4::F16>(a, s);
+  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, WAVES, S, e4::F32>(a, s);
   return EAGLE4_NOT_COVERED;
 }
 
@@ -248,13 +508,26 @@ extern "C" int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* a, void* 
       !e4::is_float_dtype(a->out_dtype) || !e4::is_float_dtype(a->h0_dtype) || a->snap_indices.ptr == nullptr ||
       a->parents.ptr == nullptr || a->cu_seqlens.ptr == nullptr || a->h0_indices.ptr == nullptr)
     return EAGLE4_NOT_COVERED;
+  // q, k, v rows are read in 4-element chunks
+  const int64_t esz = a->in_dtype == EAGLE4_F32 ? 4 : 2;
+  if (a->stride_q % 4 || a->stride_k % 4 || a->stride_v % 4 || reinterpret_cast<uintptr_t>(a->q) % (4 * esz) ||
+      reinterpret_cast<uintptr_t>(a->k) % (4 * esz) || reinterpret_cast<uintptr_t>(a->v) % (4 * esz))
+    return EAGLE4_NOT_COVERED;
+  // 4 waves per workgroup; up to 16 state values per lane and stack slot (16 KB of LDS per slot and workgroup)
   switch (a->K) {
-    case 8: return launch_in<8, 2, 1>(*a, s);
-    case 16: return launch_in<16, 4, 1>(*a, s);
-    case 32: return launch_in<32, 8, 1>(*a, s);
-    case 64: return launch_in<64, 8, 2>(*a, s);
-    case 128: return launch_in<128, 8, 4>(*a, s);
-    case 256: return launch_in<256, 8, 2>(*a, s);
+    case 8: return launch_in<8, 2, 1, 4, 4>(*a, s);
+    case 16: return launch_in<16, 4, 1, 4, 4>(*a, s);
+    case 32: return launch_in<32, 8, 1, 4, 4>(*a, s);
+    case 64: return launch_in<64, 8, 1, 4, 4>(*a, s);
+#ifndef E4_GDN_RPT
+#define E4_GDN_RPT 2
+#define E4_GDN_S 2
+#endif
+#ifndef E4_GDN_WAVES
+#define E4_GDN_WAVES 4
+#endif
+    case 128: return launch_in<128, 8, E4_GDN_RPT, E4_GDN_WAVES, E4_GDN_S>(*a, s);
+    case 256: return launch_in<256, 16, 1, 4, 2>(*a, s);
     default: return EAGLE4_NOT_COVERED;
   }
 }

@@ -37,25 +37,25 @@ def _state_close(got, want):
     torch.testing.assert_close(got.float(), want.float(), atol=1e-5, rtol=1e-4)
 
 
-@pytest.mark.parametrize("parent_lists", [[TREE, CHAIN], [TREE, TREE[:5]], [_random_tree(16, 2), _random_tree(16, 3)]])
-@pytest.mark.parametrize("dims", [(2, 4, 8, 8), (2, 6, 128, 128), (1, 2, 64, 32), (4, 8, 256, 128)])
-def test_vllm_row_slots_fp32_match_oracle(dev, parent_lists, dims):
-    """The reference test's layout (tests/test_gdn_tree_kernels.py:179-219): fp32 inputs, one slot per row."""
+def _vllm_case(dev, parent_lists, dims, state_dtype=torch.float32, edit_slots=None, seed=1):
+    """One slot per row (the vLLM layout); runs the GPU walk and the oracle walk on the same inputs and compares."""
     from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
 
-    announce(f"recurrence vllm fp32 dims={dims} widths={[len(p) for p in parent_lists]}")
-    gen = torch.Generator().manual_seed(1)
+    gen = torch.Generator().manual_seed(seed)
     width = max(map(len, parent_lists))
-    (heads, value_heads, dk, dv), num_slots = dims, 40
+    (heads, value_heads, dk, dv) = dims
     parents, qsl = _requests(parent_lists, width)
     tokens = int(qsl[-1])
     q, k = torch.randn(1, tokens, heads, dk, generator=gen), torch.randn(1, tokens, heads, dk, generator=gen)
     v = torch.randn(1, tokens, value_heads, dv, generator=gen)
     a, b = torch.randn(tokens, value_heads, generator=gen), torch.randn(tokens, value_heads, generator=gen)
     A_log, dt_bias = torch.randn(value_heads, generator=gen), torch.randn(value_heads, generator=gen)
-    state = torch.randn(num_slots, value_heads, dv, dk, generator=gen) * 0.1
     slots = torch.arange(1, 1 + len(parent_lists) * (width + 1), dtype=torch.int32).view(len(parent_lists), width + 1)
-    accepted = torch.tensor([1, 2][: len(parent_lists)], dtype=torch.int32)
+    if edit_slots is not None:
+        edit_slots(slots)
+    num_slots = int(slots.max()) + 2
+    state = (torch.randn(num_slots, value_heads, dv, dk, generator=gen) * 0.1).to(state_dtype)
+    accepted = torch.tensor([1 + (i % 2) for i in range(len(parent_lists))], dtype=torch.int32)
     kw = dict(num_accepted_tokens=accepted, pad_slot_id=0)
     s_want = state.clone()
     o_want = orr.gdn_tree_recurrent_update(A_log, dt_bias, q, k, v, a, b, initial_state_source=s_want,
@@ -70,8 +70,51 @@ def test_vllm_row_slots_fp32_match_oracle(dev, parent_lists, dims):
                                       intermediate_state_indices=g["slots"], retrieve_parent_token=g["parents"],
                                       num_accepted_tokens=g["accepted"], pad_slot_id=0)
     torch.cuda.synchronize()
-    torch.testing.assert_close(o_got.cpu(), o_want, atol=1e-4, rtol=1e-4)
-    _state_close(g["state"].cpu(), s_want)
+    if state_dtype == torch.float32:
+        torch.testing.assert_close(o_got.cpu(), o_want, atol=1e-4, rtol=1e-4)
+        _state_close(g["state"].cpu(), s_want)
+    else:  # 16-bit snapshots: within one rounding of the oracle's (the fp32 math differs in summation order)
+        torch.testing.assert_close(o_got.cpu().float(), o_want.float(), atol=2e-2, rtol=1e-2)
+        torch.testing.assert_close(g["state"].cpu().float(), s_want.float(), atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("parent_lists", [[TREE, CHAIN], [TREE, TREE[:5]], [_random_tree(16, 2), _random_tree(16, 3)]])
+@pytest.mark.parametrize("dims", [(2, 4, 8, 8), (2, 6, 128, 128), (1, 2, 64, 32), (4, 8, 256, 128)])
+def test_vllm_row_slots_fp32_match_oracle(dev, parent_lists, dims):
+    """The reference test's layout (tests/test_gdn_tree_kernels.py:179-219): fp32 inputs, one slot per row."""
+    announce(f"recurrence vllm fp32 dims={dims} widths={[len(p) for p in parent_lists]}")
+    _vllm_case(dev, parent_lists, dims)
+
+
+# Nodes 0..5 each have two children, the lower-index one leading deeper, so six states are parked at once (more
+# than the walk's LDS stack holds: the deepest ones are reloaded from their snapshots).
+NESTED = [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5]
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_nested_branches_beyond_the_parked_states(dev, state_dtype):
+    announce(f"recurrence nested branches {state_dtype}")
+    _vllm_case(dev, [NESTED, _random_tree(16, 4)], (2, 4, 128, 128), state_dtype=state_dtype)
+
+
+def _pad_row(slots):
+    slots[0, 3] = 0  # row 3's snapshot is not written; its children continue from the previous row's state
+
+
+def _shared_slot(slots):
+    slots[1, 5] = slots[1, 2]  # rows 2 and 5 share a slot: row 2's later children read row 5's snapshot
+
+
+@pytest.mark.parametrize("case", ["pad_row", "shared_slot", "long_request"])
+def test_reference_index_order_for_other_slot_tables(dev, case):
+    """Slot tables whose reloads do not return the parent's own state keep the reference's index-order walk
+    (kernels/gdn_tree_recurrence.py:312-329), as does a request of more than 64 rows."""
+    announce(f"recurrence index-order walk {case}")
+    if case == "long_request":
+        _vllm_case(dev, [_random_tree(80, 6), TREE], (1, 2, 64, 32))
+    else:
+        _vllm_case(dev, [_random_tree(16, 7), _random_tree(16, 8)], (2, 4, 128, 128),
+                   edit_slots=_pad_row if case == "pad_row" else _shared_slot)
 
 
 @pytest.mark.parametrize("batch", [1, 4])
