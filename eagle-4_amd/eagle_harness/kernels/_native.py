@@ -121,9 +121,9 @@ class GdnArgs(ctypes.Structure):
 class RecordsArgs(ctypes.Structure):
     _fields_ = _fields(
         "q:p k:p v:p stride_q:q stride_k:q stride_v:q in_dtype:i gate_dtype:i a:p b:p stride_a:q stride_b:q "
-        "A_log:p dt_bias:p A_log_dtype:i dt_bias_dtype:i scale:f out_dtype:i out:p state:p stride_state:q "
-        "state_dtype:i round_state:i state_indices:t query_start_loc:t parent:t records:p stride_records_row:q "
-        "rec:i width:i record_indices:t N:i H:i HV:i K:i V:i reserved:i"
+        "A_log:p dt_bias:p A_log_dtype:i dt_bias_dtype:i scale:f out_dtype:i out:p stride_o:q state:p "
+        "stride_state:q state_dtype:i path_replay:i state_indices:t query_start_loc:t parent:t tree_paths:t "
+        "records:p stride_records_row:q record_indices:t rec:i width:i num_paths:i N:i H:i HV:i K:i V:i"
     )
 
 

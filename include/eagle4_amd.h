@@ -159,32 +159,38 @@ typedef struct eagle4_gdn_args {
 } eagle4_gdn_args;
 int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* args, void* stream);
 
-/* ---- GDN records contract: kernels/gdn_tree_records.py:16-101, 104-156, 160-272, 364-444 --------------------------- */
+/* ---- GDN records contract: kernels/gdn_tree_records.py:16-101, 104-156, 160-272, 276-361, 364-444 ------------------
+ * Per node a replay record (delta [V], normalised key [K], decay exp(g); REC >= V + K + 1 floats) instead of a state
+ * snapshot. path_replay = 1 is gdn_tree_records_update with tree_paths (replaces _gdn_tree_pre_kernel +
+ * _gdn_tree_records_kernel, :16-156, 364-444): the tree comes from the path table, every parent state is rounded
+ * to the pool dtype before its children read it, a request with record row < 0 is one chain without rounding.
+ * path_replay = 0 is gdn_tree_chunk_update (replaces _gdn_tree_chunk_kernel, :276-361, 496-579): the tree comes from
+ * `parent`, no rounding (fp32 pools); a node whose parent is outside the request starts from the pool state. */
 typedef struct eagle4_records_args {
-  const void *q, *k, *v;
+  const void *q, *k, *v; /* q, k (1, tokens, H, K); v (1, tokens, HV, V); token-strided, unit inner strides */
   int64_t stride_q, stride_k, stride_v;
   int32_t in_dtype, gate_dtype;
-  const void *a, *b;
+  const void *a, *b; /* (tokens, HV) */
   int64_t stride_a, stride_b;
-  const void *A_log, *dt_bias;
+  const void *A_log, *dt_bias; /* [HV] */
   int32_t A_log_dtype, dt_bias_dtype;
   float scale;
   int32_t out_dtype;
-  void* out; /* (1, tokens, HV, V) contiguous */
-  const void* state; /* pool [slots, HV, V, K] */
+  void* out; /* (1, tokens, HV, V), contiguous over (HV, V) */
+  int64_t stride_o;
+  const void* state; /* pool [slots, HV, V, K], contiguous (V, K) per head */
   int64_t stride_state;
   int32_t state_dtype;
-  int32_t round_state;
-  eagle4_itab state_indices;   /* [N] */
+  int32_t path_replay;
+  eagle4_itab state_indices;   /* [N]; < 0: start from zeros */
   eagle4_itab query_start_loc; /* [N + 1] */
-  eagle4_itab parent;          /* [N, >= width] */
+  eagle4_itab parent;          /* [N, >= width] (chunk form) */
+  eagle4_itab tree_paths;      /* [N, P, 2 + width] int32, s0 / s1 the request / path strides, entries contiguous */
   float* records;              /* [rows, steps, HV, REC] fp32 */
   int64_t stride_records_row;
-  int32_t rec;
-  int32_t width;
-  eagle4_itab record_indices; /* [N] */
+  eagle4_itab record_indices; /* [N]; < 0: no records for the request */
+  int32_t rec, width, num_paths;
   int32_t N, H, HV, K, V;
-  int32_t reserved;
 } eagle4_records_args;
 int eagle4_gdn_tree_records_update(const eagle4_records_args* args, void* stream);
 

@@ -1,0 +1,210 @@
+"""The GDN records contract on the GPU against the oracle (kernels/gdn_tree_records.py): the path replay with its
+parent rounding for 16-bit and fp32 pools, a request without records run as one chain, the fp32 chunk form, the
+accepted-path commit over layers (rounded and not), and the commit of the chunk form landing on the snapshot walk's
+accepted state. Outputs within the output dtype's tolerance, fp32 records and states within 1e-4 relative."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import records as orec
+from oracle import recurrence as orr
+from oracle.tables import _gdn_tree_paths
+from workloads import seeded_tree
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = -999.0
+
+
+def _inputs(parent_lists, heads, value_heads, dk, dv, pool_dtype, in_dtype=torch.bfloat16, seed=0, width=None):
+    gen = torch.Generator().manual_seed(seed)
+    N = len(parent_lists)
+    width = width or max(map(len, parent_lists))
+    qsl = [0]
+    for p in parent_lists:
+        qsl.append(qsl[-1] + len(p))
+    tokens = qsl[-1]
+    parent = torch.zeros(N, width, dtype=torch.int32)
+    paths = np.zeros((N, width, 2 + width), dtype=np.int32)
+    for n, p in enumerate(parent_lists):
+        parent[n, : len(p)] = torch.tensor(p)
+        parent[n, 0] = -1
+        _gdn_tree_paths(list(p) + [0] * (width - len(p)), len(p), width, paths[n])
+    inp = dict(
+        q=torch.randn(1, tokens, heads, dk, generator=gen).to(in_dtype),
+        k=torch.randn(1, tokens, heads, dk, generator=gen).to(in_dtype),
+        v=torch.randn(1, tokens, value_heads, dv, generator=gen).to(in_dtype),
+        a=torch.randn(tokens, value_heads, generator=gen).to(in_dtype),
+        b=torch.randn(tokens, value_heads, generator=gen).to(in_dtype),
+        A_log=torch.randn(value_heads, generator=gen) * 0.5,
+        dt_bias=torch.randn(value_heads, generator=gen) * 0.5,
+        state=(torch.randn(N + 3, value_heads, dv, dk, generator=gen) * 0.1).to(pool_dtype),
+        state_indices=torch.tensor([n + 2 for n in range(N)], dtype=torch.int32),
+        query_start_loc=torch.tensor(qsl, dtype=torch.int32),
+        parent=parent,
+        tree_paths=torch.from_numpy(paths),
+        records=torch.full((N + 1, width, value_heads, dv + dk + 4), SENTINEL),
+        record_indices=torch.tensor([N - n for n in range(N)], dtype=torch.int32),  # rows in reverse
+    )
+    return inp, width
+
+
+def _to(d, dev):
+    return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+def _call(fn, inp, width, **kw):
+    return fn(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"], inp["b"], state=inp["state"],
+              state_indices=inp["state_indices"], query_start_loc=inp["query_start_loc"], parent=inp["parent"],
+              records=inp["records"], record_indices=inp["record_indices"], width=width, **kw)
+
+
+def _compare(got_out, want_out, got_rec, want_rec, fp32_exact, K, V):
+    tol = dict(atol=1e-4, rtol=1e-4) if fp32_exact else dict(atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(got_out.cpu().float(), want_out.float(), **tol)
+    got_rec = got_rec.cpu()
+    written = want_rec[..., 0] != SENTINEL
+    assert torch.equal(got_rec[..., 0] != SENTINEL, written)  # the same nodes written, sentinels elsewhere
+    torch.testing.assert_close(got_rec[..., :V][written], want_rec[..., :V][written], **tol)  # delta
+    torch.testing.assert_close(got_rec[..., V : V + K + 1][written], want_rec[..., V : V + K + 1][written],
+                               atol=1e-5, rtol=1e-5)  # key and decay
+    assert torch.all(got_rec[..., V + K + 1 :] == SENTINEL)  # the record's spare floats are never written
+
+
+@pytest.mark.parametrize("pool_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_path_replay_matches_oracle(dev, pool_dtype):
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
+
+    announce(f"records path replay pool={pool_dtype}")
+    rng = np.random.default_rng(2)
+    trees = [seeded_tree(rng, 16), [-1, 0, 1, 2, 3, 4], [-1, 0, 0, 1, 1, 2, 3, 5], seeded_tree(rng, 12)]
+    inp, width = _inputs(trees, 4, 8, 128, 128, pool_dtype, seed=3)
+    want_rec = inp["records"].clone()
+    want = orec.gdn_tree_records_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"],
+                                        inp["b"], state=inp["state"], state_indices=inp["state_indices"],
+                                        query_start_loc=inp["query_start_loc"], parent=inp["parent"],
+                                        tree_paths=inp["tree_paths"], records=want_rec,
+                                        record_indices=inp["record_indices"], width=width)
+    g = _to(inp, dev)
+    got = _call(gdn_tree_records_update, g, width, tree_paths=g["tree_paths"])
+    torch.cuda.synchronize()
+    _compare(got, want, g["records"], want_rec, pool_dtype == torch.float32, 128, 128)
+    assert torch.equal(g["state"].cpu(), inp["state"])  # the verify never writes the pool
+
+
+def test_request_without_records_runs_as_one_chain(dev):
+    """record_indices < 0: no records, and the replay runs the request's rows as one chain without rounding
+    (kernels/gdn_tree_records.py:51-53), whatever its tree."""
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
+
+    announce("records chain rows")
+    rng = np.random.default_rng(5)
+    trees = [seeded_tree(rng, 16), seeded_tree(rng, 10)]
+    inp, width = _inputs(trees, 2, 4, 64, 32, torch.bfloat16, seed=6)
+    inp["record_indices"] = torch.tensor([-1, 1], dtype=torch.int32)
+    want_rec = inp["records"].clone()
+    want = orec.gdn_tree_records_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"],
+                                        inp["b"], state=inp["state"], state_indices=inp["state_indices"],
+                                        query_start_loc=inp["query_start_loc"], parent=inp["parent"],
+                                        tree_paths=inp["tree_paths"], records=want_rec,
+                                        record_indices=inp["record_indices"], width=width)
+    g = _to(inp, dev)
+    got = _call(gdn_tree_records_update, g, width, tree_paths=g["tree_paths"])
+    torch.cuda.synchronize()
+    _compare(got, want, g["records"], want_rec, False, 64, 32)
+
+
+@pytest.mark.parametrize("dims", [(4, 8, 128, 128), (2, 2, 64, 32), (1, 2, 256, 128)])
+def test_chunk_form_matches_oracle_closed_form(dev, dims):
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
+
+    announce(f"records chunk form dims={dims}")
+    rng = np.random.default_rng(7)
+    trees = [seeded_tree(rng, 16), [-1, 0, 1, 1, 0], seeded_tree(rng, 9)]
+    inp, width = _inputs(trees, *dims, torch.float32, seed=8)
+    want_rec = inp["records"].clone()
+    want = orec.gdn_tree_chunk_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"], inp["b"],
+                                      state=inp["state"], state_indices=inp["state_indices"],
+                                      query_start_loc=inp["query_start_loc"], parent=inp["parent"], records=want_rec,
+                                      record_indices=inp["record_indices"], width=width)
+    g = _to(inp, dev)
+    got = _call(gdn_tree_records_update, g, width, tree_paths=None)  # fp32 pool without paths: the chunk form
+    torch.cuda.synchronize()
+    _compare(got, want, g["records"], want_rec, True, dims[2], dims[3])
+
+
+def test_deep_branching_replays_unparked_parents(dev):
+    """More nested branches than the walk parks: the deepest parents are recomputed from the pool state."""
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
+
+    announce("records deep branching")
+    nested = [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5]
+    for pool_dtype in (torch.bfloat16, torch.float32):
+        inp, width = _inputs([nested, nested[:9]], 2, 4, 128, 128, pool_dtype, seed=9)
+        want_rec = inp["records"].clone()
+        want = orec.gdn_tree_records_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"],
+                                            inp["b"], state=inp["state"], state_indices=inp["state_indices"],
+                                            query_start_loc=inp["query_start_loc"], parent=inp["parent"],
+                                            tree_paths=inp["tree_paths"], records=want_rec,
+                                            record_indices=inp["record_indices"], width=width)
+        g = _to(inp, dev)
+        got = _call(gdn_tree_records_update, g, width, tree_paths=g["tree_paths"])
+        torch.cuda.synchronize()
+        _compare(got, want, g["records"], want_rec, pool_dtype == torch.float32, 128, 128)
+
+
+@pytest.mark.parametrize("pool_dtype,round_state", [(torch.bfloat16, True), (torch.float32, False),
+                                                    (torch.float16, True)])
+def test_commit_matches_oracle_over_layers(dev, pool_dtype, round_state):
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_commit
+
+    announce(f"records commit pool={pool_dtype} round={round_state}")
+    gen = torch.Generator().manual_seed(11)
+    layers, N, width, HV, K, V = 2, 4, 8, 4, 128, 128
+    parent = torch.tensor([[-1, 0, 0, 1, 1, 2, 3, 5]] * N, dtype=torch.int32)
+    state = (torch.randn(layers, N + 2, HV, V, K, generator=gen) * 0.1).to(pool_dtype)
+    records = torch.randn(layers, N + 1, width, HV, V + K + 4, generator=gen) * 0.1
+    records[..., V + K] = torch.rand(layers, N + 1, width, HV, generator=gen) * 0.5 + 0.5  # decays in (0.5, 1)
+    state_indices = torch.tensor([1, 2, -1, 4], dtype=torch.int32)  # request 2: no slot
+    record_indices = torch.tensor([3, 0, 1, 2], dtype=torch.int32)
+    commit_steps = torch.tensor([7, 0, 5, -1], dtype=torch.int32)  # request 3: nothing accepted
+    want = state.clone()
+    orec.gdn_tree_records_commit(want, records, state_indices, record_indices, commit_steps, parent, round_state)
+    got = state.to(dev)
+    gdn_tree_records_commit(got, records.to(dev), state_indices.to(dev), record_indices.to(dev),
+                            commit_steps.to(dev), parent.to(dev), round_state)
+    torch.cuda.synchronize()
+    tol = dict(atol=1e-5, rtol=1e-4) if pool_dtype == torch.float32 else dict(atol=1e-2, rtol=1e-2)
+    torch.testing.assert_close(got.cpu().float(), want.float(), **tol)
+    untouched = [0, 3, 4, 5]  # slots no committed request names
+    assert torch.equal(got.cpu()[:, untouched], state[:, untouched])
+
+
+def test_chunk_then_commit_lands_on_the_walks_accepted_state(dev):
+    """fp32: the chunk form's records folded along an accepted path give the snapshot walk's state of that node."""
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_commit, gdn_tree_records_update
+
+    announce("records chunk + commit vs walk")
+    tree = [-1, 0, 0, 1, 2, 4, 4, 3]
+    accepted = 6
+    inp, width = _inputs([tree], 2, 4, 128, 128, torch.float32, seed=12)
+    g = _to(inp, dev)
+    _call(gdn_tree_records_update, g, width, tree_paths=None)
+    pool = g["state"].clone()[None]  # one layer
+    gdn_tree_records_commit(pool, g["records"][None], g["state_indices"], g["record_indices"],
+                            torch.tensor([accepted], dtype=torch.int32, device=dev), g["parent"], False)
+    torch.cuda.synchronize()
+    # the oracle walk with one snapshot slot per row
+    T = len(tree)
+    snaps = torch.zeros(2 + T, 4, 128, 128)
+    snaps[1] = inp["state"][int(inp["state_indices"][0])]
+    slots = torch.arange(1, T + 2, dtype=torch.int32)[None]
+    orr.gdn_tree_recurrent_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"], inp["b"],
+                                  initial_state_source=snaps, initial_state_indices=slots,
+                                  cu_seqlens=inp["query_start_loc"], intermediate_states_buffer=snaps,
+                                  intermediate_state_indices=slots, retrieve_parent_token=inp["parent"],
+                                  num_accepted_tokens=torch.tensor([1], dtype=torch.int32), pad_slot_id=0)
+    want = snaps[int(slots[0, accepted])]
+    torch.testing.assert_close(pool[0, int(inp["state_indices"][0])].cpu(), want, atol=1e-5, rtol=1e-4)
