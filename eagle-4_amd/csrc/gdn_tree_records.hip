@@ -53,108 +53,105 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_records_walk_kernel(const eagl
     lrow[s] = wave * ROWS_WAVE + s * (64 / C) + rr;
     rows[s] = row0 + lrow[s];
   }
-  const int64_t bos = e4::ld(a.query_start_loc, n);
-  const int T = static_cast<int>(e4::ld(a.query_start_loc, n + 1) - bos);
+  // the request's tables first, all in flight together
+  const int64_t bos = uni64(e4::ld(a.query_start_loc, n));
+  const int64_t eos = uni64(e4::ld(a.query_start_loc, n + 1));
+  const int64_t rec_idx = uni64(e4::ld(a.record_indices, n));
+  const int64_t idx = uni64(e4::ld(a.state_indices, n));
+  const uint32_t A_raw = load_raw(a.A_log, hv, a.A_log_dtype);
+  const uint32_t dt_raw = load_raw(a.dt_bias, hv, a.dt_bias_dtype);
+  const int T = static_cast<int>(eos - bos);
   if (T <= 0) return;
-  const int64_t rec_idx = e4::ld(a.record_indices, n);
   const bool chain = a.path_replay && rec_idx < 0;  // a request without records: one chain, no rounding (:51-53)
   const bool round = !kPoolExact && a.path_replay && rec_idx >= 0;
   const int Tn = chain ? T : (T < a.width ? T : a.width);  // nodes walked: a tree has at most width (<= 64) rows
-  // the per-token values of the pre kernel (:104-156): softplus beta 1, threshold 20
-  const float A = -expf(e4::load_scalar(a.A_log, hv, a.A_log_dtype));
-  const float dt_bias = e4::load_scalar(a.dt_bias, hv, a.dt_bias_dtype);
 
-  // the initial state: the request's pool slot, zeros for a negative index (:73-75)
+  // The prologue issues every load before its first wait: the initial state (the request's pool slot, zeros for a
+  // negative index, :73-75), the staged nodes' inputs, the parent table, then the path table.
   float h[RPT][E];
-  const int64_t idx = e4::ld(a.state_indices, n);
+  uint4 h0raw[RPT][NJ];
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
-  auto load_h0 = [&]() {
+  auto issue_h0 = [&]() {
 #pragma unroll
-    for (int s = 0; s < RPT; ++s) {
+    for (int s = 0; s < RPT; ++s)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        if (idx >= 0 && rows[s] < a.V) {
-          load4_code(a.state, idx * a.stride_state + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
-                     a.state_dtype, &h[s][4 * j]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[s][e + 4 * j] = 0.f;
-        }
+        h0raw[s][j] = make_uint4(0u, 0u, 0u, 0u);  // zero bits: +0.0 in every dtype
+        if (idx >= 0 && rows[s] < a.V)
+          load_state_raw(a.state, idx * a.stride_state + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
+                         a.state_dtype, h0raw[s][j]);
       }
-    }
   };
-  load_h0();
+  auto widen_h0 = [&]() {
+#pragma unroll
+    for (int s = 0; s < RPT; ++s)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) widen_state_raw(h0raw[s][j], a.state_dtype, &h[s][4 * j]);
+  };
+  auto load_h0 = [&]() {
+    issue_h0();
+    settle_loads();
+    widen_h0();
+  };
+  issue_h0();
+  const int ts = Tn < TS ? Tn : TS;
+  Staging<Tin, K, TS, ROWS, NT> stg;
+  const NodeSrc src{a.q, a.k, a.v, a.a, a.b, a.stride_q, a.stride_k, a.stride_v, a.stride_a, a.stride_b,
+                    a.gate_dtype, ih, hv, a.V};
+  stg.issue(src, bos, ts, row0, tid);
+  int par = -2;
+  if (!chain && !a.path_replay && lane < Tn) par = lane == 0 ? -1 : static_cast<int>(e4::ld(a.parent, n, lane));
 
   // The tree. Path replay: every entry (d > 0) of a path names the entry before it as its parent (:77-80); nodes on
   // no path are never visited (the replay writes nothing for them). Chunk form: `parent`, node 0 the root.
   if (!chain && a.path_replay) {
     if (tid < 64) s_par[tid] = -2;
     __syncthreads();
-    const int D = a.width;
-    for (int i = tid; i < a.num_paths * D; i += NT) {
-      const int p = i / D, d = i % D;
-      const int32_t* prow = static_cast<const int32_t*>(a.tree_paths.ptr) + n * a.tree_paths.s0 + p * a.tree_paths.s1;
-      const int L = prow[0];
-      if (d < L && d < D) {
-        const int tok = prow[2 + d];
-        const int prev = d > 0 ? prow[1 + d] : -1;
-        if (tok >= 0 && tok < Tn && prev >= -1 && prev < Tn && prev != tok) s_par[tok] = prev;
+    const int D = a.width, PD = a.num_paths * a.width;
+    for (int base = 0; base < PD; base += 4 * NT) {  // 4 entries per thread in flight
+      int L[4], tok[4], prev[4], dd[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = base + j * NT + tid;
+        L[j] = 0;
+        tok[j] = -1;
+        prev[j] = -1;
+        dd[j] = 0;
+        if (i < PD) {
+          const int p = i / D, d = i % D;
+          const int32_t* prow = static_cast<const int32_t*>(a.tree_paths.ptr) + n * a.tree_paths.s0 + p * a.tree_paths.s1;
+          dd[j] = d;
+          L[j] = prow[0];
+          tok[j] = prow[2 + d];
+          if (d > 0) prev[j] = prow[1 + d];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (dd[j] < L[j] && tok[j] >= 0 && tok[j] < Tn && prev[j] >= -1 && prev[j] < Tn && prev[j] != tok[j])
+          s_par[tok[j]] = prev[j];
       }
     }
   }
 
-  // ---- staging: q, k, v and the node scalars of nodes [0, min(Tn, TS)) -------------------------------------------
-  const int ts = Tn < TS ? Tn : TS;
-  {
-    constexpr int CH = K / 4;
-    for (int i = tid; i < ts * CH; i += NT) {
-      const int t = i / CH, ch = i % CH;
-      const int64_t tok = bos + t;
-      *reinterpret_cast<Raw4<Tin>*>(&s_q[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
-          static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K + 4 * ch);
-      *reinterpret_cast<Raw4<Tin>*>(&s_k[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
-          static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K + 4 * ch);
-    }
-    for (int i = tid; i < ts * ROWS; i += NT) {
-      const int t = i / ROWS, r = i % ROWS;
-      const int row = row0 + r < a.V ? row0 + r : a.V - 1;  // rows past V are computed and dropped
-      s_v[t][r] = static_cast<const IS*>(a.v)[(bos + t) * a.stride_v + static_cast<int64_t>(hv) * a.V + row];
-    }
-    if (tid < ts) {
-      const float2 g = gate_of(load_raw(a.a, (bos + tid) * a.stride_a + hv, a.gate_dtype),
-                               load_raw(a.b, (bos + tid) * a.stride_b + hv, a.gate_dtype), a.gate_dtype, 1.0f, 20.0f,
-                               A, dt_bias);
-      s_sc[tid] = make_float4(g.x, g.y, 0.f, 0.f);
-    }
-  }
+  // ---- staging: q, k, v and the node scalars of nodes [0, ts) into LDS --------------------------------------------
+  // the per-token values of the pre kernel (:104-156): softplus beta 1, threshold 20
+  const float A = -expf(widen_raw(A_raw, a.A_log_dtype));
+  const float dt_bias = widen_raw(dt_raw, a.dt_bias_dtype);
+  stg.commit(s_q, s_k, s_v, s_sc, ts, tid, a.gate_dtype, 1.0f, 20.0f, A, dt_bias);
+  widen_h0();
   __syncthreads();
-  for (int t = wave; t < ts; t += WAVES) {  // L2 norms over K, one node per wave
-    float qq = 0.f, kk = 0.f;
-    for (int e = lane; e < K; e += 64) {
-      const float qv = Tin::to_f32(s_q[t][e]), kv = Tin::to_f32(s_k[t][e]);
-      qq = fmaf(qv, qv, qq);
-      kk = fmaf(kv, kv, kk);
-    }
-    qq = e4::group_sum<64>(qq);
-    kk = e4::group_sum<64>(kk);
-    if (lane == 0) {
-      s_sc[t].z = a.scale / sqrtf(qq + 1e-6f);
-      s_sc[t].w = 1.0f / sqrtf(kk + 1e-6f);
-    }
-  }
+  stage_norms<Tin, K, TS, NT>(s_q, s_k, s_sc, ts, tid, a.scale);
   __syncthreads();
 
   // lane i: node i's parent (-1 a root: starts from the pool state; -2 not in the tree), children and the roots
-  int par = -2;
   uint64_t kids = 0, roots = 0;
   if (!chain) {
     if (lane < Tn) {
-      if (a.path_replay) {
+      if (a.path_replay)
         par = s_par[lane];
-      } else {
-        par = lane == 0 ? -1 : static_cast<int>(e4::ld(a.parent, n, lane));
-        if (lane > 0 && (par < 0 || par >= Tn || par == lane)) par = -1;  // outside the request: no ancestors
-      }
+      else if (lane > 0 && (par < 0 || par >= Tn || par == lane))
+        par = -1;  // outside the request: no ancestors
     }
     for (int i = 0; i < Tn; ++i) {
       const uint64_t m = __ballot(lane < Tn && par == i);

@@ -74,12 +74,16 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     for (int i = tid; i < a.num_slot_cols; i += NT)
       a.publish[n * a.stride_publish + i] = static_cast<int32_t>(e4::ld(a.snap_indices, n, i));
   }
-  const int64_t bos = e4::ld(a.cu_seqlens, n);
-  const int T = static_cast<int>(e4::ld(a.cu_seqlens, n + 1) - bos);
+  // The prologue issues every load before its first wait: the request's tables, the plan tables (parents, slots),
+  // the initial state, the staged nodes' inputs; the plan is computed while the last of them are in flight.
+  const int64_t bos = uni64(e4::ld(a.cu_seqlens, n));
+  const int64_t eos = uni64(e4::ld(a.cu_seqlens, n + 1));
+  const int64_t cache_idx = uni64(e4::ld(a.snap_indices, n, 0));  // the request's scratch row (per-row slots: row 0's)
+  const int64_t nacc = a.num_accepted.ptr != nullptr ? uni64(e4::ld(a.num_accepted, n)) : 1;
+  const uint32_t A_raw = load_raw(a.A_log, hv, a.A_log_dtype);
+  const uint32_t dt_raw = load_raw(a.dt_bias, hv, a.dt_bias_dtype);
+  const int T = static_cast<int>(eos - bos);
   if (T <= 0) return;
-  const int64_t cache_idx = e4::ld(a.snap_indices, n, 0);  // the request's scratch row (per-row slots: row 0's slot)
-  const float A = -expf(e4::load_scalar(a.A_log, hv, a.A_log_dtype));
-  const float dt_bias = e4::load_scalar(a.dt_bias, hv, a.dt_bias_dtype);
 
   // The walk plan: lane i holds row i's parent, slot and children (a bit mask). Depth first needs reloads that
   // return the parent's own snapshot.
@@ -92,63 +96,24 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     if (a.row_slots) my_slot = e4::ld(a.snap_indices, n, lane);
   }
   // the initial state (:284-296); with num_accepted its slot is in column num_accepted - 1
-  float h[RPT][E];
-  const int64_t idx = a.num_accepted.ptr != nullptr ? e4::ld(a.h0_indices, n, e4::ld(a.num_accepted, n) - 1)
-                                                    : e4::ld(a.h0_indices, n, 0);
+  const int64_t idx = uni64(e4::ld(a.h0_indices, n, nacc - 1));
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
+  float h[RPT][E];
+  uint4 h0raw[RPT][NJ];
 #pragma unroll
-  for (int s = 0; s < RPT; ++s) {
+  for (int s = 0; s < RPT; ++s)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      if (idx > a.pad_slot_id && rows[s] < a.V) {
-        load4_code(a.h0_source, idx * a.stride_h0_source + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
-                   a.h0_dtype, &h[s][4 * j]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[s][e + 4 * j] = 0.f;
-      }
+      h0raw[s][j] = make_uint4(0u, 0u, 0u, 0u);  // zero bits: +0.0 in every dtype
+      if (idx > a.pad_slot_id && rows[s] < a.V)
+        load_state_raw(a.h0_source, idx * a.stride_h0_source + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
+                       a.h0_dtype, h0raw[s][j]);
     }
-  }
-  // ---- staging: q, k, v and the node scalars of nodes [0, min(T, TS)) --------------------------------------------
   const int ts = T < TS ? T : TS;
-  {
-    constexpr int CH = K / 4;  // Raw4 chunks per q / k row
-    for (int i = tid; i < ts * CH; i += NT) {
-      const int t = i / CH, ch = i % CH;
-      const int64_t tok = bos + t;
-      *reinterpret_cast<Raw4<Tin>*>(&s_q[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
-          static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K + 4 * ch);
-      *reinterpret_cast<Raw4<Tin>*>(&s_k[t][4 * ch]) = *reinterpret_cast<const Raw4<Tin>*>(
-          static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K + 4 * ch);
-    }
-    for (int i = tid; i < ts * ROWS; i += NT) {
-      const int t = i / ROWS, r = i % ROWS;
-      const int row = row0 + r < a.V ? row0 + r : a.V - 1;  // rows past V are computed and dropped
-      s_v[t][r] = static_cast<const IS*>(a.v)[(bos + t) * a.stride_v + static_cast<int64_t>(hv) * a.V + row];
-    }
-    if (tid < ts) {
-      const float2 g = gate_of(load_raw(a.a, (bos + tid) * a.stride_a + hv, a.gate_dtype),
-                               load_raw(a.b, (bos + tid) * a.stride_b + hv, a.gate_dtype), a.gate_dtype,
-                               a.softplus_beta, a.softplus_threshold, A, dt_bias);
-      s_sc[tid] = make_float4(g.x, g.y, 0.f, 0.f);
-    }
-  }
-  __syncthreads();
-  for (int t = wave; t < ts; t += WAVES) {  // L2 norms over K (:143-151), one node per wave
-    float qq = 0.f, kk = 0.f;
-    for (int e = lane; e < K; e += 64) {
-      const float qv = Tin::to_f32(s_q[t][e]), kv = Tin::to_f32(s_k[t][e]);
-      qq = fmaf(qv, qv, qq);
-      kk = fmaf(kv, kv, kk);
-    }
-    qq = e4::group_sum<64>(qq);
-    kk = e4::group_sum<64>(kk);
-    if (lane == 0) {
-      s_sc[t].z = a.scale / sqrtf(qq + 1e-6f);
-      s_sc[t].w = 1.0f / sqrtf(kk + 1e-6f);
-    }
-  }
-  __syncthreads();
+  Staging<Tin, K, TS, ROWS, NT> stg;
+  const NodeSrc src{a.q, a.k, a.v, a.a, a.b, a.stride_q, a.stride_k, a.stride_v, a.stride_a, a.stride_b,
+                    a.gate_dtype, ih, hv, a.V};
+  stg.issue(src, bos, ts, row0, tid);
 
   if (dfs) {
     bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot <= a.pad_slot_id);
@@ -166,6 +131,18 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
       }
     }
   }
+
+  // ---- staging: q, k, v and the node scalars of nodes [0, ts) into LDS --------------------------------------------
+  const float A = -expf(widen_raw(A_raw, a.A_log_dtype));
+  const float dt_bias = widen_raw(dt_raw, a.dt_bias_dtype);
+  stg.commit(s_q, s_k, s_v, s_sc, ts, tid, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
+#pragma unroll
+  for (int s = 0; s < RPT; ++s)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) widen_state_raw(h0raw[s][j], a.h0_dtype, &h[s][4 * j]);
+  __syncthreads();
+  stage_norms<Tin, K, TS, NT>(s_q, s_k, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
+  __syncthreads();
 
   settle_loads();  // the initial state and the plan tables
   // A node's inputs: staged ones from LDS, later ones (T > TS) from global memory with their scalars computed here.
@@ -293,7 +270,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
       if (dfs) {
         slot = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), u));
       } else {
-        slot = e4::ld(a.snap_indices, n, u);
+        slot = uni64(e4::ld(a.snap_indices, n, u));
         settle_loads();
       }
     }
@@ -357,8 +334,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
         }
       } else {
         // the reference's rule (:312-329)
-        const int p = static_cast<int>(e4::ld(a.parents, n, next));
-        const int64_t pslot = a.row_slots && p >= 0 ? e4::ld(a.snap_indices, n, p) : cache_idx;
+        const int p = uni(static_cast<int>(e4::ld(a.parents, n, next)));
+        const int64_t pslot = a.row_slots && p >= 0 ? uni64(e4::ld(a.snap_indices, n, p)) : cache_idx;
         bool re = p >= 0 && pslot > a.pad_slot_id;
         if (a.skip_chain_reload) re = re && p != next - 1;
         if (re) reload(snap_at(pslot, p));

@@ -98,6 +98,15 @@ E4_DEV float2 gate_of(uint32_t a_raw, uint32_t b_raw, int gate_dtype, float soft
 E4_DEV void settle_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 E4_DEV int readlane(int x, int l) { return __builtin_amdgcn_readlane(x, l); }
+
+// A value every lane holds the same copy of (a request's table entries), moved to a scalar register so the code
+// that depends on it (the walk's loop bounds and branches) is compiled as wave-uniform, not per lane.
+E4_DEV int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+E4_DEV int64_t uni64(int64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint64_t>(x) & 0xffffffffu));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint64_t>(x) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 E4_DEV uint64_t readlane64(uint64_t x, int l) {
   const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(x & 0xffffffffu), l);
   const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(x >> 32), l);
@@ -112,5 +121,133 @@ struct Node {
   typename Tin::storage v[RPT];
   float4 sc;
 };
+
+}  // namespace e4walk
+
+namespace e4walk {
+
+// ---- a walk's prologue: every load issued before the first wait -------------------------------------------------
+// Four state values of a runtime dtype as raw bits (16 bytes of fp32, or 8 bytes of a 16-bit dtype in .x / .y),
+// widened later: a conversion next to each load would make every load wait for the one before.
+E4_DEV void load_state_raw(const void* base, int64_t off, int dtype, uint4& r) {
+  if (dtype == EAGLE4_F32) {
+    r = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+  } else {
+    const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+    r = make_uint4(t.x, t.y, 0u, 0u);
+  }
+}
+
+E4_DEV void widen_state_raw(const uint4& r, int dtype, float* out) {
+  if (dtype == EAGLE4_F32) {
+    out[0] = __uint_as_float(r.x);
+    out[1] = __uint_as_float(r.y);
+    out[2] = __uint_as_float(r.z);
+    out[3] = __uint_as_float(r.w);
+  } else {
+    const uint16_t v[4] = {static_cast<uint16_t>(r.x & 0xffffu), static_cast<uint16_t>(r.x >> 16),
+                           static_cast<uint16_t>(r.y & 0xffffu), static_cast<uint16_t>(r.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = dtype == EAGLE4_BF16 ? e4::bf16_to_f32(v[e]) : e4::f16_to_f32(v[e]);
+  }
+}
+
+// Where a request's node inputs live: q, k rows of its key head, v rows of its value head, gate inputs.
+struct NodeSrc {
+  const void *q, *k, *v, *a, *b;
+  int64_t stride_q, stride_k, stride_v, stride_a, stride_b;
+  int gate_dtype, ih, hv, V;
+};
+
+// The inputs of nodes [0, ts) of a request (ts <= TS), loaded by NT threads into registers (issue) and then written
+// to LDS (commit), so all their loads are in flight together. The workgroup's V rows are [row0, row0 + ROWS).
+template <typename Tin, int K, int TS, int ROWS, int NT>
+struct Staging {
+  using IS = typename Tin::storage;
+  static constexpr int CH = K / 4;  // Raw4 chunks per q / k row
+  static constexpr int QK_IT = (TS * CH + NT - 1) / NT;
+  static constexpr int V_IT = (TS * ROWS + NT - 1) / NT;
+  Raw4<Tin> q[QK_IT], k[QK_IT];
+  IS v[V_IT];
+  uint32_t ga, gb;
+
+  E4_DEV void issue(const NodeSrc& s, int64_t bos, int ts, int row0, int tid) {
+#pragma unroll
+    for (int it = 0; it < QK_IT; ++it) {
+      const int i = tid + it * NT;
+      if (i < ts * CH) {
+        const int t = i / CH, ch = i % CH;
+        const int64_t tok = bos + t;
+        q[it] = *reinterpret_cast<const Raw4<Tin>*>(static_cast<const IS*>(s.q) + tok * s.stride_q +
+                                                    static_cast<int64_t>(s.ih) * K + 4 * ch);
+        k[it] = *reinterpret_cast<const Raw4<Tin>*>(static_cast<const IS*>(s.k) + tok * s.stride_k +
+                                                    static_cast<int64_t>(s.ih) * K + 4 * ch);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < V_IT; ++it) {
+      const int i = tid + it * NT;
+      if (i < ts * ROWS) {
+        const int t = i / ROWS, r = i % ROWS;
+        const int row = row0 + r < s.V ? row0 + r : s.V - 1;  // rows past V are computed and dropped
+        v[it] = static_cast<const IS*>(s.v)[(bos + t) * s.stride_v + static_cast<int64_t>(s.hv) * s.V + row];
+      }
+    }
+    if (tid < ts) {
+      ga = load_raw(s.a, (bos + tid) * s.stride_a + s.hv, s.gate_dtype);
+      gb = load_raw(s.b, (bos + tid) * s.stride_b + s.hv, s.gate_dtype);
+    }
+  }
+
+  E4_DEV void commit(IS (&s_q)[TS][K], IS (&s_k)[TS][K], IS (&s_v)[TS][ROWS], float4 (&s_sc)[TS], int ts, int tid,
+                     int gate_dtype, float softplus_beta, float softplus_threshold, float A, float dt_bias) {
+#pragma unroll
+    for (int it = 0; it < QK_IT; ++it) {
+      const int i = tid + it * NT;
+      if (i < ts * CH) {
+        const int t = i / CH, ch = i % CH;
+        *reinterpret_cast<Raw4<Tin>*>(&s_q[t][4 * ch]) = q[it];
+        *reinterpret_cast<Raw4<Tin>*>(&s_k[t][4 * ch]) = k[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < V_IT; ++it) {
+      const int i = tid + it * NT;
+      if (i < ts * ROWS) s_v[i / ROWS][i % ROWS] = v[it];
+    }
+    if (tid < ts) {
+      const float2 g = gate_of(ga, gb, gate_dtype, softplus_beta, softplus_threshold, A, dt_bias);
+      s_sc[tid] = make_float4(g.x, g.y, 0.f, 0.f);
+    }
+  }
+};
+
+// L2 norms over K of the staged nodes (kernels/gdn_tree_recurrence.py:143-151), all nodes at once: NT / TS
+// adjacent threads share a node, each summing a contiguous run of its q and k; .z = scale / |q|, .w = 1 / |k|
+// (1e-6 inside the square roots).
+template <typename Tin, int K, int TS, int NT>
+E4_DEV void stage_norms(const typename Tin::storage (&s_q)[TS][K], const typename Tin::storage (&s_k)[TS][K],
+                        float4 (&s_sc)[TS], int ts, int tid, float scale) {
+  constexpr int LPN0 = NT / TS < 64 ? NT / TS : 64;
+  constexpr int LPN = LPN0 < K ? LPN0 : K;  // threads per node (a power of two)
+  constexpr int PER = K / LPN;                       // elements each
+  static_assert(PER >= 1 && K % LPN == 0, "norm split");
+  const int t = tid / LPN, part = tid % LPN;
+  float qq = 0.f, kk = 0.f;
+  if (t < ts) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const float qv = Tin::to_f32(s_q[t][part * PER + e]), kv = Tin::to_f32(s_k[t][part * PER + e]);
+      qq = fmaf(qv, qv, qq);
+      kk = fmaf(kv, kv, kk);
+    }
+  }
+  qq = e4::group_sum<LPN>(qq);
+  kk = e4::group_sum<LPN>(kk);
+  if (t < ts && part == 0) {
+    s_sc[t].z = scale / sqrtf(qq + 1e-6f);
+    s_sc[t].w = 1.0f / sqrtf(kk + 1e-6f);
+  }
+}
 
 }  // namespace e4walk

@@ -559,7 +559,9 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
 }
 
 // Merges the pieces of each segment cut by share boundaries (vllm/verify_attention.py:115-139): weights
-// 2^(lse_i - max) over the pieces' normalised fp32 partials. One workgroup per segment.
+// 2^(lse_i - max) over the pieces' normalised fp32 partials. A workgroup takes 256 (row, 4 columns) items of one
+// segment, one item per thread, and folds the pieces in one pass with a running max, so a thread's loads do not
+// wait on each other.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_args a, const StreamPlan p) {
   const int s = blockIdx.x;
@@ -572,40 +574,42 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
   const int64_t start = pre[b] * p.HR + k * tiles, end = start + tiles;
   const int64_t w0 = ((start + 1) * nact - 1) / tiles_all, w1 = (end * nact - 1) / tiles_all;
   if (w0 == w1) return;  // inside one share: written directly
-  const int G = p.G, kvh = k / p.RG, rg = k - kvh * p.RG;
+  constexpr int TPR = D / 4;
+  const int item = blockIdx.y * 256 + threadIdx.x;
   const int rows_seg = p.rows_seg;
+  if (item >= rows_seg * TPR) return;
+  const int r = item / TPR, d = 4 * (item % TPR);
+  const int G = p.G, kvh = k / p.RG, rg = k - kvh * p.RG;
   const int64_t qs = e4::ld(a.query_start_loc, b);
   int64_t rows = e4::ld(a.query_start_loc, b + 1) - qs;
   rows = rows < a.max_query_len ? rows : a.max_query_len;
-  constexpr int TPR = D / 4;
-  for (int item = threadIdx.x; item < rows_seg * TPR; item += 256) {
-    const int r = item / TPR, d = 4 * (item % TPR);
-    const int rho = rg * rows_seg + r;
-    const int rt = rho / 16;
-    const int t = rho / G, gq = rho - t * G;
-    if (rt >= p.row_tiles || t >= rows) continue;
-    float mx = -INFINITY;
-    for (int64_t wi = w0; wi <= w1; ++wi) mx = fmaxf(mx, a.workspace[p.lse_off + (s + wi) * rows_seg + r]);
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-    float wsum = 0.f;
-    for (int64_t wi = w0; wi <= w1; ++wi) {
-      const int64_t part = (s + wi) * rows_seg + r;
-      const float ls = a.workspace[p.lse_off + part];
-      const float wt = ls == -INFINITY ? 0.f : exp2f(ls - mx);
-      const float4 v = *reinterpret_cast<const float4*>(a.workspace + p.part_off + part * D + d);
-      sum.x += wt * v.x;
-      sum.y += wt * v.y;
-      sum.z += wt * v.z;
-      sum.w += wt * v.w;
-      wsum += wt;
-    }
-    const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-    uint2 o;
-    o.x = pack2<T>(sum.x * inv, sum.y * inv);
-    o.y = pack2<T>(sum.z * inv, sum.w * inv);
-    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + (qs + t) * a.stride_ot +
-                              (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d) = o;
+  const int rho = rg * rows_seg + r;
+  const int rt = rho / 16;
+  const int t = rho / G, gq = rho - t * G;
+  if (rt >= p.row_tiles || t >= rows) return;
+  float mx = -INFINITY, wsum = 0.f;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int64_t wi = w0; wi <= w1; ++wi) {
+    const int64_t part = (s + wi) * rows_seg + r;
+    const float ls = a.workspace[p.lse_off + part];
+    const float4 v = *reinterpret_cast<const float4*>(a.workspace + p.part_off + part * D + d);
+    if (ls == -INFINITY) continue;  // a piece with no visible key
+    const float m_new = fmaxf(mx, ls);
+    const float keep = exp2f(mx - m_new), wt = exp2f(ls - m_new);
+    sum.x = sum.x * keep + wt * v.x;
+    sum.y = sum.y * keep + wt * v.y;
+    sum.z = sum.z * keep + wt * v.z;
+    sum.w = sum.w * keep + wt * v.w;
+    wsum = wsum * keep + wt;
+    mx = m_new;
   }
+  const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+  uint2 o;
+  o.x = pack2<T>(sum.x * inv, sum.y * inv);
+  o.y = pack2<T>(sum.z * inv, sum.w * inv);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + (qs + t) * a.stride_ot +
+                            (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d) = o;
 }
 
 template <int D, int C, typename T>
@@ -647,7 +651,8 @@ int groups(const eagle4_attn_args& a, int c) {
 template <int D, int C, typename T>
 int launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
   verify_stream_kernel<D, C, T><<<p.nwg, 64 * (C + kProducers), 0, s>>>(a, p);
-  verify_stream_merge<D, T><<<a.num_reqs * p.HR, 256, 0, s>>>(a, p);
+  verify_stream_merge<D, T><<<dim3(a.num_reqs * p.HR, e4::ceil_div(static_cast<int64_t>(p.rows_seg) * (D / 4), 256)), 256, 0,
+                               s>>>(a, p);
   return E4_LAUNCH_STATUS();
 }
 
