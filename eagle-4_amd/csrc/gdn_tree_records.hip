@@ -19,6 +19,11 @@
 
 #include "gdn_walk.h"
 
+namespace e4chunk {
+// gdn_tree_chunk.hip: the chunk form on the matrix cores (trees of <= 16 nodes, bf16 inputs)
+int launch(const eagle4_records_args& a, hipStream_t s) __attribute__((visibility("hidden")));
+}
+
 namespace {
 
 using namespace e4walk;
@@ -485,6 +490,10 @@ extern "C" int eagle4_gdn_tree_records_update(const eagle4_records_args* a, void
       reinterpret_cast<uintptr_t>(a->q) % (4 * esz) || reinterpret_cast<uintptr_t>(a->k) % (4 * esz) ||
       reinterpret_cast<uintptr_t>(a->v) % (4 * esz))
     return EAGLE4_NOT_COVERED;
+  if (!a->path_replay) {
+    const int st = e4chunk::launch(*a, s);
+    if (st != EAGLE4_NOT_COVERED) return st;
+  }
   switch (a->K) {
     case 8: return launch_records<8, 2, 1, 2, 4>(*a, s);
     case 16: return launch_records<16, 4, 1, 2, 4>(*a, s);
