@@ -11,8 +11,9 @@ A step is one pass of the hot path over one batch of synthetic input, resident i
      compaction, state move) for seeded accept lengths U[1, 12].
 
 ``value`` = 64 x 16 verified tokens per step / step time. The JSON line also carries the dominant kernel's
-roofline (algorithmic HBM bytes per launch / its HIP-event duration, against MI355X's 8 TB/s) and the CPU baseline
-(the oracle, timed on a bounded sample on this host's cores). ``--calibrate-copy`` instead times a plain 1 GiB
+roofline (algorithmic HBM bytes per launch / its HIP-event duration, against MI355X's 8 TB/s), the CPU baseline
+(the oracle, timed on a bounded sample on this host's cores) and the records contract's chunk form per layer at
+1 / 4 / 16 / 32 requests beside the reference's published times (``--records-only`` prints just that). ``--calibrate-copy`` instead times a plain 1 GiB
 device copy (the reference kernel for the rocprofv3 FETCH_SIZE / WRITE_SIZE scale).
 """
 
@@ -100,6 +101,54 @@ def _cpu_baseline(work, sample: int, seconds: float) -> dict:
                       f"GDN walk with fp32 snapshots, commit), {passes} passes in {dt:.1f} s on {threads} host threads"}
 
 
+# The reference's published MI355X figures for the records chunk form (FlyDSL, per layer, TP1 H16/HV48, K = V = 128,
+# 16-node trees, bf16 pool; eagle_harness/kernels/gdn_tree_chunk_flydsl.py:25-27), microseconds by request count.
+RECORDS_PUBLISHED_US = {1: 10.5, 4: 11.9, 16: 23.8, 32: 34.7}
+
+
+def _records_chunk(steps: int) -> dict:
+    """The records contract's chunk form (one GDN layer's verify writing replay records) at 1 / 4 / 16 / 32 requests:
+    the time per call of a HIP graph of 5 calls, best of 3 replays of ``steps`` graphs."""
+    import torch
+
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_chunk_update
+    from workloads import RECORDS_BATCHES, records_inputs
+
+    dev = torch.device("cuda:0")
+    us = {}
+    for batch in RECORDS_BATCHES:
+        x = records_inputs(batch, seed=batch, device=dev)
+
+        def call():
+            gdn_tree_chunk_update(x["A_log"], x["dt_bias"], x["q"], x["k"], x["v"], x["a"], x["b"], state=x["state"],
+                                  state_indices=x["state_indices"], query_start_loc=x["query_start_loc"],
+                                  parent=x["parent"], records=x["records"], record_indices=x["record_indices"],
+                                  width=x["width"])
+
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        reps = 5
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                call()
+        best = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                g.replay()
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / (steps * reps))
+        us[batch] = best
+        del x, g
+    return {"workload": "GDN records chunk form per layer: H16/HV48 K=V=128, 16-node trees, bf16 pool, bf16 q/k/v",
+            "us_per_call": us, "reference_published_us": RECORDS_PUBLISHED_US,
+            "speedup_vs_reference": {b: RECORDS_PUBLISHED_US[b] / us[b] for b in us}}
+
+
 def _calibrate_copy(steps: int) -> None:
     import torch
 
@@ -128,6 +177,7 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=64, help="requests in the CPU baseline's sample (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the CPU baseline runs whole passes this long")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--records-only", action="store_true", help="time only the records chunk form and print it")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -138,6 +188,9 @@ def main() -> int:
 
     if args.calibrate_copy:
         _calibrate_copy(args.steps)
+        return 0
+    if args.records_only:
+        print(json.dumps({"records_chunk": _records_chunk(args.steps)}), flush=True)
         return 0
 
     from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
@@ -312,6 +365,7 @@ def main() -> int:
         "kernels": kernels,
         "cpu_baseline": _cpu_baseline(work, args.cpu_sample, args.cpu_seconds) if work is not None else None,
     }
+    result["records_chunk"] = _records_chunk(args.steps)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -35,9 +35,11 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-file additions. The streamed attention kernel keeps its MFMA accumulators in VGPRs (the default AGPR form makes
-# LLVM shuttle them between the two files every iteration at this register pressure).
-EXTRA_FLAGS = {"verify_attention_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Per-file additions. The streamed attention and tree-chunk kernels keep their MFMA accumulators in VGPRs (the default
+# AGPR form makes LLVM shuttle them between the two register files: every iteration in the attention kernel, for every
+# accumulator the chunk kernel's VALU math reads).
+EXTRA_FLAGS = {"verify_attention_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+               "gdn_tree_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _hipcc() -> str:

@@ -217,10 +217,18 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
       kr[kb] = *reinterpret_cast<const uint4*>(kp + 32 * kb);
     }
   }
+  // v before the pool slice: loads complete in order, and the first tile needs v but only its own slice part
+  const int v0 = slice * 16 * NTL;
+  Run16<NTL> vr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = 4 * g + r;
+    const int64_t ti = bos + (i < T ? i : T - 1);
+    vr[r].load(static_cast<const uint16_t*>(a.v) + ti * a.stride_v + static_cast<int64_t>(hv) * a.V + v0 + NTL * c);
+  }
   // The pool slice (rows v0 .. v0 + 16 NTL of the request's slot) through a buffer resource whose range is the slice,
   // or empty for a negative slot index: its loads then return zeros, the zero initial state (:341-345), with no
   // branch around them.
-  const int v0 = slice * 16 * NTL;
   using PS = typename Tpool::storage;
   constexpr int kSliceBytes = 16 * NTL * K * static_cast<int>(sizeof(PS));
   const char* slot = static_cast<const char*>(a.state) +
@@ -238,35 +246,19 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
         const int off = ((NTL * c + u) * K + 32 * kb + 8 * g) * static_cast<int>(sizeof(PS)) + 16 * q;
         sraw[u][kb][q] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(srsrc, off, 0, 0));
       }
-  Run16<NTL> vr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = 4 * g + r;
-    const int64_t ti = bos + (i < T ? i : T - 1);
-    vr[r].load(static_cast<const uint16_t*>(a.v) + ti * a.stride_v + static_cast<int64_t>(hv) * a.V + v0 + NTL * c);
-  }
   // keep the scheduler from sinking these loads below the per-node math that waits for the q / k rows
   __builtin_amdgcn_sched_barrier(0);
 
-  // ---- per node: norms, gates, ancestors, root-path log decay --------------------------------------------------------
-  float qq = 0.f, kk = 0.f;
+  // ---- node x node products; their diagonals are the squared norms ---------------------------------------------------
+  f32x4_t KK = {0.f, 0.f, 0.f, 0.f}, KQ = {0.f, 0.f, 0.f, 0.f}, QQ = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
-    const uint32_t qw[4] = {qr[kb].x, qr[kb].y, qr[kb].z, qr[kb].w};
-    const uint32_t kw[4] = {kr[kb].x, kr[kb].y, kr[kb].z, kr[kb].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qq = fmaf(lo_bf16(qw[e]), lo_bf16(qw[e]), qq);
-      qq = fmaf(hi_bf16(qw[e]), hi_bf16(qw[e]), qq);
-      kk = fmaf(lo_bf16(kw[e]), lo_bf16(kw[e]), kk);
-      kk = fmaf(hi_bf16(kw[e]), hi_bf16(kw[e]), kk);
-    }
+    KK = mma_bf16(kr[kb], kr[kb], KK);  // KK[i][j] = k_i . k_j
+    KQ = mma_bf16(kr[kb], qr[kb], KQ);  // KQ[i][j] = k_i . q_j
+    QQ = mma_bf16(qr[kb], qr[kb], QQ);  // QQ[i][j] = q_i . q_j
   }
-  qq += __shfl_xor(qq, 16, 64);
-  qq += __shfl_xor(qq, 32, 64);
-  kk += __shfl_xor(kk, 16, 64);
-  kk += __shfl_xor(kk, 32, 64);
-  const float qs = a.scale / sqrtf(qq + 1e-6f), ks = 1.0f / sqrtf(kk + 1e-6f);  // (:147-150)
+
+  // ---- per node (lane c): gates, ancestors, root-path log decay -----------------------------------------------------
   const float A = -expf(widen_word(A_w, a.A_log_dtype));
   const float dt_bias = widen_word(dt_w, a.dt_bias_dtype);
   const uint32_t ga_raw = a.gate_dtype == EAGLE4_F32 ? ga.w : (ga.w >> ga.sh) & 0xffffu;
@@ -275,11 +267,12 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
   const float decay = c < T ? gt.x : 1.0f, beta = c < T ? gt.y : 0.0f;  // past the tree: exp(g) 1, beta 0 (:316-317)
   // a parent outside the tree (or the node itself) makes the node a root
   const int par = c > 0 && c < T && par_raw >= 0 && par_raw < T && par_raw != c ? par_raw : -1;
-  // pointer jumping: after round j, anc holds the ancestors at distance 1 .. 2^j, lsum the log decays of the node and
-  // its ancestors at distance < 2^j, jmp the ancestor at distance 2^j (-1 past the root); depth < 16 needs 4 rounds
+  // pointer jumping: after round j, anc holds the ancestors at distance 1 .. 2^j, lsum the log2 decays of the node and
+  // its ancestors at distance < 2^j, jmp the ancestor at distance 2^j (-1 past the root); depth < 16 needs 4 rounds.
+  // Decay ratios are then powers of two of log2 differences (the hardware exp2 / log2, ~1 ulp).
   uint32_t anc = par >= 0 ? 1u << par : 0u;
   int jmp = par;
-  float lsum = logf(fmaxf(decay, 1e-30f));
+  float lsum = __builtin_amdgcn_logf(fmaxf(decay, 1e-30f));
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int src = jmp >= 0 ? jmp : c;
@@ -292,20 +285,32 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
       jmp = jmp_j;
     }
   }
-  const float logG = lsum;
-  if (g == 0) {
-    s_nd[c] = make_float4(ks, qs, beta, logG);
+  const float logG = lsum;  // log2 G
+  // node c's squared norms sit on the diagonals at lane (c / 4, c), element c % 4; that lane publishes the node
+  const int rc = c & 3;
+  const float kk = rc == 0 ? KK[0] : rc == 1 ? KK[1] : rc == 2 ? KK[2] : KK[3];
+  const float qq = rc == 0 ? QQ[0] : rc == 1 ? QQ[1] : rc == 2 ? QQ[2] : QQ[3];
+  if (g == (c >> 2)) {
+    s_nd[c] = make_float4(1.0f / sqrtf(kk + 1e-6f), a.scale / sqrtf(qq + 1e-6f), beta, logG);  // (:147-150)
     s_anc[c] = anc;
   }
   __syncthreads();
-
-  // ---- node x node matrices ------------------------------------------------------------------------------------------
-  f32x4_t KK = {0.f, 0.f, 0.f, 0.f}, KQ = {0.f, 0.f, 0.f, 0.f};
+  const float ks = s_nd[c].x, qs = s_nd[c].y;
+  // the record's key and decay (once per node and value head) leave now, ahead of the matrix work
+  float* rec = a.records + static_cast<int64_t>(rec_row) * a.stride_records_row;
+  if (slice == 0 && rec_row >= 0 && c < T) {
+    float* p = rec + (static_cast<int64_t>(c) * a.HV + hv) * a.rec + a.V;
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    KK = mma_bf16(kr[kb], kr[kb], KK);  // KK[i][j] = k_i . k_j
-    KQ = mma_bf16(kr[kb], qr[kb], KQ);  // KQ[i][j] = k_i . q_j
+    for (int kb = 0; kb < KB; ++kb) {
+      const uint4 x = kr[kb];
+      float4* d = reinterpret_cast<float4*>(p + 32 * kb + 8 * g);
+      d[0] = make_float4(lo_bf16(x.x) * ks, hi_bf16(x.x) * ks, lo_bf16(x.y) * ks, hi_bf16(x.y) * ks);
+      d[1] = make_float4(lo_bf16(x.z) * ks, hi_bf16(x.z) * ks, lo_bf16(x.w) * ks, hi_bf16(x.w) * ks);
+    }
+    if (g == 0) p[K] = decay;
   }
+
+  // ---- L, L^T, W^T -------------------------------------------------------------------------------------------------
   float4 nd[4];
   float Gr[4];
   f32x4_t L, LT, WT, I;
@@ -314,14 +319,14 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
     const int i = 4 * g + r;
     nd[r] = s_nd[i];
     const uint32_t anc_i = s_anc[i];
-    Gr[r] = expf(nd[r].w);
+    Gr[r] = __builtin_amdgcn_exp2f(nd[r].w);
     const bool c_above_i = (anc_i >> c) & 1u;  // c a strict ancestor of i
     const bool i_above_c = (anc >> i) & 1u;    // i a strict ancestor of c
     const float kk_n = nd[r].x * ks * KK[r];
     // L[i][c] = beta_i G_i / G_c k^_i . k^_c on strict ancestors c of i
-    L[r] = c_above_i ? nd[r].z * expf(nd[r].w - logG) * kk_n : 0.f;
+    L[r] = c_above_i ? nd[r].z * __builtin_amdgcn_exp2f(nd[r].w - logG) * kk_n : 0.f;
     // L^T[i][c] = L[c][i];  W^T[i][c] = W[c][i] = G_c / G_i q^_c . k^_i on ancestors-or-self i of c
-    const float ratio = i_above_c || i == c ? expf(logG - nd[r].w) : 0.f;
+    const float ratio = i_above_c || i == c ? __builtin_amdgcn_exp2f(logG - nd[r].w) : 0.f;
     LT[r] = i_above_c ? beta * ratio * kk_n : 0.f;
     WT[r] = ratio * (qs * nd[r].x * KQ[r]);
     I[r] = i == c ? 1.f : 0.f;
@@ -364,7 +369,6 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
 
   // ---- stores --------------------------------------------------------------------------------------------------------
   const int64_t col = static_cast<int64_t>(hv) * a.V + v0 + NTL * c;
-  float* rec = a.records + static_cast<int64_t>(rec_row) * a.stride_records_row;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = 4 * g + r;
@@ -372,17 +376,6 @@ __global__ __launch_bounds__(64) void gdn_chunk_kernel(const eagle4_records_args
       store_run_out<NTL>(a.out, (bos + i) * a.stride_o + col, a.out_dtype, O[r]);
       if (rec_row >= 0) store_run_f32<NTL>(rec + (static_cast<int64_t>(i) * a.HV + hv) * a.rec + v0 + NTL * c, D[r]);
     }
-  }
-  if (slice == 0 && rec_row >= 0 && c < T) {  // the key and decay of the record, once per (node, value head)
-    float* p = rec + (static_cast<int64_t>(c) * a.HV + hv) * a.rec + a.V;
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      const uint4 x = kr[kb];
-      float4* d = reinterpret_cast<float4*>(p + 32 * kb + 8 * g);
-      d[0] = make_float4(lo_bf16(x.x) * ks, hi_bf16(x.x) * ks, lo_bf16(x.y) * ks, hi_bf16(x.y) * ks);
-      d[1] = make_float4(lo_bf16(x.z) * ks, hi_bf16(x.z) * ks, lo_bf16(x.w) * ks, hi_bf16(x.w) * ks);
-    }
-    if (g == 0) p[K] = decay;
   }
 }
 
@@ -410,7 +403,8 @@ int launch_pool(const eagle4_records_args& a, hipStream_t s) {
 
 template <int K>
 int launch_k(const eagle4_records_args& a, hipStream_t s) {
-  // columns per wave: enough waves to fill the chip (~2 per SIMD) before a wave takes more columns
+  // columns per wave: more columns per wave once there are enough waves to keep HBM busy (measured at 16 / 48 heads,
+  // K = V = 128: 1 tile per wave at 1 request, 2 at 4, 4 at 16 and 32)
   const int64_t pairs = static_cast<int64_t>(a.N) * a.HV;
   const bool fp32_pool = a.state_dtype == EAGLE4_F32;
 #ifdef E4_CHUNK_NTL
@@ -418,8 +412,8 @@ int launch_k(const eagle4_records_args& a, hipStream_t s) {
   if (a.V % (16 * forced) == 0) return launch_pool<K, forced>(a, s);
 #endif
   if constexpr (K <= 128)
-    if (!fp32_pool && a.V % 64 == 0 && pairs * (a.V / 64) >= 2048) return launch_pool<K, 4>(a, s);
-  if (a.V % 32 == 0 && pairs * (a.V / 32) >= 2048) return launch_pool<K, 2>(a, s);
+    if (!fp32_pool && a.V % 64 == 0 && pairs * (a.V / 64) >= 1024) return launch_pool<K, 4>(a, s);
+  if (a.V % 32 == 0 && pairs * (a.V / 32) >= 512) return launch_pool<K, 2>(a, s);
   return launch_pool<K, 1>(a, s);
 }
 

@@ -217,6 +217,35 @@ def gdn_inputs(shape: GdnShape, seed: int, device="cpu", layout: str = "vllm", s
     return {kk: (vv.to(device) if isinstance(vv, torch.Tensor) else vv) for kk, vv in out.items()}
 
 
+# The records contract's chunk form at the 27B-class TP1 layer (16 key / 48 value heads, K = V = 128), 16-node trees.
+RECORDS_BATCHES = (1, 4, 16, 32)
+
+
+def records_inputs(batch: int, seed: int, device="cpu", pool_dtype=torch.bfloat16, heads: int = 16,
+                   value_heads: int = 48, dk: int = 128, dv: int = 128, width: int = 16) -> dict:
+    """Inputs of one GDN layer's records verify: ``batch`` seeded ``width``-node trees, q/k/v/a/b ~ N(0,1) (bf16),
+    A_log = dt_bias = 0, a pool of ``batch + 1`` slots ~ N(0, 0.02^2) (request n reads slot n + 1), records
+    [batch, width, HV, V + K + 4] fp32 (request n writes row n)."""
+    rng = np.random.default_rng(seed)
+    gen = torch.Generator(device=device).manual_seed(seed + 1)
+    tokens = batch * width
+    trees = [seeded_tree(rng, width) for _ in range(batch)]
+
+    def r(*shape):
+        return torch.randn(*shape, device=device, generator=gen)
+
+    return dict(
+        q=r(1, tokens, heads, dk).bfloat16(), k=r(1, tokens, heads, dk).bfloat16(),
+        v=r(1, tokens, value_heads, dv).bfloat16(), a=r(tokens, value_heads).bfloat16(),
+        b=r(tokens, value_heads).bfloat16(), A_log=torch.zeros(value_heads, device=device),
+        dt_bias=torch.zeros(value_heads, device=device), state=(r(batch + 1, value_heads, dv, dk) * 0.02).to(pool_dtype),
+        state_indices=torch.arange(1, batch + 1, dtype=torch.int32, device=device),
+        query_start_loc=torch.arange(0, tokens + 1, width, dtype=torch.int32, device=device),
+        parent=torch.tensor(trees, dtype=torch.int32, device=device),
+        records=torch.zeros(batch, width, value_heads, dv + dk + 4, device=device),
+        record_indices=torch.arange(batch, dtype=torch.int32, device=device), width=width, trees=trees)
+
+
 def accept_paths(parents_list: list[list[int]], seed: int, width: int) -> tuple[torch.Tensor, torch.Tensor]:
     """Seeded accept lengths U[1, 12] -> (path [B, W] int32, path_len [B] int32) of the committed node's root path."""
     rng = np.random.default_rng(seed + 7)
