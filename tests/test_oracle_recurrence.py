@@ -103,6 +103,41 @@ def test_walk_matches_the_chunk_closed_form():
                                        rtol=1e-4)
 
 
+def test_chunk_form_is_independent_of_node_order():
+    """The chunk form takes the nodes in any order (kernels/gdn_tree_records.py:276-361 builds the ancestor closure
+    from the parent links): relabelling a tree's non-root nodes, with their rows moved along, moves the outputs and
+    records the same way."""
+    shape = GdnShape(2, 12, 2, 4, 32, 16)
+    inp = gdn_inputs(shape, seed=9, layout="sglang", in_dtype=torch.float32)
+    rng = np.random.default_rng(10)
+    W = shape.width
+    # new label of old node j, per request (the root keeps 0)
+    labels = [[0] + [int(x) for x in rng.permutation(np.arange(1, W))] for _ in range(shape.batch)]
+    rows = torch.arange(shape.batch * W)
+    parent = inp["parent_table"].clone()
+    for n, lab in enumerate(labels):
+        for j in range(W):
+            rows[n * W + lab[j]] = n * W + j  # new row lab[j] holds old row j
+            if j > 0:
+                parent[n, lab[j]] = lab[int(inp["parent_table"][n, j])]
+    moved = {key: inp[key][:, rows] if key in ("q", "k", "v") else inp[key][rows] for key in ("q", "k", "v", "a", "b")}
+
+    def run(q, k, v, a, b, par):
+        rec = torch.full((shape.batch, W, shape.hv, shape.v + shape.k + 4), -999.0)
+        out = orec.gdn_tree_chunk_update(inp["A_log"], inp["dt_bias"], q, k, v, a, b, state=inp["pool"],
+                                         state_indices=inp["state_indices"], query_start_loc=inp["query_start_loc"],
+                                         parent=par, records=rec, record_indices=inp["scratch_indices"], width=W)
+        return out, rec
+
+    out, rec = run(inp["q"], inp["k"], inp["v"], inp["a"], inp["b"], inp["parent_table"])
+    out2, rec2 = run(moved["q"], moved["k"], moved["v"], moved["a"], moved["b"], parent)
+    assert any(int(parent[n, t]) > t for n in range(shape.batch) for t in range(1, W))  # not parent-first
+    torch.testing.assert_close(out2[0], out[0, rows], atol=1e-5, rtol=1e-5)
+    node_rows = torch.tensor([[lab.index(t) for t in range(W)] for lab in labels])  # old node at each new label
+    for n in range(shape.batch):
+        torch.testing.assert_close(rec2[n], rec[n, node_rows[n]], atol=1e-5, rtol=1e-5)
+
+
 def test_single_step_closed_form():
     """From S0 = 0, one node: S = beta v k^T, o = beta v (k . q) scale (normalised q, k)."""
     shape = GdnShape(1, 1, 1, 2, 8, 4)
