@@ -11,11 +11,12 @@
 //
 // One wave per (request, value head, slice of 16 NTL value columns), 16 nodes on the 16 rows of the 16x16 MFMA
 // accumulator (lane (g, c), element r: row 4 g + r, column c):
-//   - everything the wave reads is issued first: parents, gates, q / k rows, the pool slice, v;
-//   - per node (lane c): norms, decay / beta, and by pointer jumping over the parent links the ancestor set (a 16-bit
-//     mask) and the root-path log-decay sum log G;
-//   - K K^T and K Q^T on v_mfma_f32_16x16x32_bf16 from the raw bf16 rows (products exact, fp32 sums; the norms are
-//     per-row factors applied afterwards), masked and scaled into L, L^T and W^T;
+//   - everything the wave reads is issued first: parents, gates, q / k rows, v, the pool slice;
+//   - K K^T, K Q^T and Q Q^T on v_mfma_f32_16x16x32_bf16 from the raw bf16 rows (products exact, fp32 sums); the
+//     squared norms are the diagonals, and the norms enter as per-row factors;
+//   - per node (lane c): decay / beta, and by pointer jumping over the parent links the ancestor set (a 16-bit mask)
+//     and the root-path log2-decay sum log2 G; the decay ratios are then hardware exp2 of log2 differences;
+//   - L, L^T and W^T masked and scaled from K K^T and K Q^T;
 //   - (I + L)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8) (L is strictly lower in the ancestor order, L^16 = 0) by 8
 //     products on v_mfma_f32_16x16x4f32, kept transposed as the left operand of D = Tinv rhs;
 //   - per 16-column tile, K S0^T and Q S0^T on the bf16 MFMA with the pool state split into exact bf16 terms

@@ -2,10 +2,11 @@
 
 The verify writes, per node and value head, a record ``(delta [V], key [K], decay)`` (``records[row, node, hv, :V]``
 the node's v' = (v - h k^) beta, ``[V:V+K]`` its normalised key, ``[V+K]`` exp(g)); the commit folds the accepted
-node's root path of records into the pool. One gfx950 kernel (``csrc/gdn_tree_records.hip``) serves both verify
-forms: the path replay (``tree_paths`` given; every parent state rounded to the pool dtype, as the reference's
-replay does) and the fp32 chunk form (no rounding) — one wave walks each (request, value head, V tile) depth first
-instead of replaying every leaf path or solving the tree in closed form; the results are the same folds.
+node's root path of records into the pool. The chunk form (no rounding) of trees with at most 16 nodes and bf16
+inputs runs in closed form on the matrix cores (``csrc/gdn_tree_chunk.hip``: one wave per (request, value head,
+column slice) solves the whole tree). The path replay (``tree_paths`` given; every parent state rounded to the pool
+dtype, as the reference's replay does) and wider trees run the depth-first walk (``csrc/gdn_tree_records.hip``: one
+wave walks each (request, value head, V tile) instead of replaying every leaf path); the results are the same folds.
 """
 
 from __future__ import annotations
