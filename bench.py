@@ -106,6 +106,174 @@ def _cpu_baseline(work, sample: int, seconds: float) -> dict:
 RECORDS_PUBLISHED_US = {1: 10.5, 4: 11.9, 16: 23.8, 32: 34.7}
 
 
+def _time_graph(fn, steps: int, reps: int = 5) -> float:
+    """Microseconds per call of ``fn``: a HIP graph of ``reps`` calls, replayed ``steps`` times between events on the
+    launch stream, best of 3."""
+    import torch
+
+    for _ in range(2):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    best = float("inf")
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / (steps * reps))
+    return best
+
+
+def _row(us: float, nbytes: int | None = None, **extra) -> dict:
+    r = {"us": round(us, 2)}
+    if nbytes:
+        r.update(bytes=nbytes, GBps=round(nbytes / (us * 1e-6) / 1e9, 1),
+                 frac_of_hbm_peak=round(nbytes / (us * 1e-6) / HBM_PEAK, 3))
+    r.update(extra)
+    return r
+
+
+def _rows(steps: int) -> dict:
+    """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
+    batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
+    attention at batch 512, the GDN walk at batch 1 and 256, 16-bit attention at batch 1, and the rounded records path
+    replay and commit. Algorithmic bytes count every element once."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from eagle_harness.kernels.accept_tail import accept_tail
+    from eagle_harness.kernels.gdn_tree import gdn_tree_ancestors
+    from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_commit, gdn_tree_records_update
+    from eagle_harness.kernels.verify_prep import tree_tail_words
+    from eagle_harness.vllm.tree_accept import accept_tree, greedy_targets
+    from eagle_harness.vllm.verify_attention import verify_attention
+    from eagle_harness.vllm.verify_layout import TreeStore
+    from workloads import (ATTN_B1, ATTN_B512_FP8, GDN_B1, GDN_B256, attention_inputs, gdn_inputs, records_inputs,
+                           seeded_tree, tree_links)
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(5)
+    rows = {}
+
+    # a9: greedy targets and the tree walk at batch 512 x 16 rows, vocab 151936 (bf16 logits, 2.49 GB)
+    B, W, vocab = 512, 16, 151936
+    logits = torch.randn(B * W, vocab, device=dev, generator=gen).bfloat16()
+    target = torch.empty(B * W, dtype=torch.int64, device=dev)
+    us = _time_graph(lambda: greedy_targets(logits, out=target), steps)
+    rows["a9_argmax_b512x16_vocab151936_bf16"] = _row(us, logits.numel() * 2 + B * W * 8)
+    rng = np.random.default_rng(11)
+    trees = [seeded_tree(rng, W) for _ in range(B)]
+    parents = torch.tensor(trees, dtype=torch.int32, device=dev)
+    drafted = torch.randint(0, vocab, (B * W,), device=dev, generator=gen)
+    cu = torch.arange(0, B * W + 1, W, dtype=torch.int32, device=dev)
+    idx = torch.arange(B, dtype=torch.int32, device=dev)
+    store = TreeStore(B, W, dev)
+    us = _time_graph(lambda: accept_tree(target, drafted, cu, idx, parents, store), steps)
+    rows["a9_accept_tree_walk_b512x16"] = _row(us, B * W * (8 + 8 + 4 + 8) + B * (4 + W * 4 + 4))
+    del logits
+
+    # a10: the bs1 accept tail over a 16-node tree (one workgroup: latency)
+    t1 = seeded_tree(rng, W)
+    nxt, sib = tree_links(t1, W)
+    tail_args = (target[:W].clone(), drafted[:W].clone(), torch.arange(W, device=dev)[None],
+                 torch.tensor([nxt], device=dev), torch.tensor([sib], device=dev), torch.tensor([4096], device=dev),
+                 torch.arange(W, device=dev) + 5000, torch.zeros(2, 8192, dtype=torch.int32, device=dev),
+                 torch.tensor([1], device=dev))
+    us = _time_graph(lambda: accept_tail(*tail_args, 12), steps)
+    rows["a10_accept_tail_bs1_w16"] = _row(us)
+
+    # a8: tail-mask words of a 16-row verify over an 8192-slot KV
+    mask = torch.randint(0, 2, (W * 8192,), device=dev, generator=gen).bool()
+    committed = torch.tensor([8192 - W], dtype=torch.int64, device=dev)
+    tail = torch.zeros(W + 1, dtype=torch.int64, device=dev)
+    us = _time_graph(lambda: tree_tail_words(mask, committed, tail, W), steps)
+    rows["a8_tail_words_w16"] = _row(us)
+
+    # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
+    for name, shape, fp8 in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True),
+                             ("a6_attention_bf16_b1_d128", ATTN_B1, False)):
+        x = attention_inputs(shape, seed=3, device=dev, fp8=fp8, gen_device=dev)
+        out = torch.empty_like(x["q"])
+        kw = dict(k_scale=x["k_scale"], v_scale=x["v_scale"]) if fp8 else {}
+
+        def attn():
+            verify_attention(x["q"], x["k_new"], x["v_new"], x["key_cache"], x["value_cache"], x["block_table"],
+                             x["context_lens"], x["query_start_loc"], x["masks"], x["scale"], out,
+                             max_query_len=shape.width, **kw)
+
+        us = _time_graph(attn, steps)
+        ctx = x["context_lens"].tolist()
+        tokens = shape.batch * shape.width
+        esz = 1 if fp8 else 2
+        nbytes = (sum(ctx) * shape.hkv * shape.d * 2 * esz + tokens * shape.hq * shape.d * 2 * 2
+                  + tokens * shape.hkv * shape.d * 2 * 2 + sum(math.ceil(L / shape.page) for L in ctx) * 4
+                  + (sum(math.ceil(L / shape.page) for L in ctx) * shape.hkv * 4 * 2 if fp8 else 0))
+        rows[name] = _row(us, nbytes)
+        del x, out
+
+    # a4: the snapshot walk at batch 1 and 256 (H16/HV32, K = V = 128, fp32 states, per-row slots)
+    for name, shape in (("a4_walk_b1", GDN_B1), ("a4_walk_b256", GDN_B256)):
+        g = gdn_inputs(shape, seed=2, device=dev, layout="vllm", gen_device=dev)
+        o = torch.empty_like(g["v"])
+
+        def walk():
+            gdn_tree_recurrent_update(g["A_log"], g["dt_bias"], g["q"], g["k"], g["v"], g["a"], g["b"],
+                                      initial_state_source=g["pool"], initial_state_indices=g["slots"],
+                                      cu_seqlens=g["query_start_loc"], intermediate_states_buffer=g["pool"],
+                                      intermediate_state_indices=g["slots"], retrieve_parent_token=g["parent_table"],
+                                      num_accepted_tokens=g["num_accepted"], pad_slot_id=0, out=o)
+
+        us = _time_graph(walk, steps)
+        Bq, Wq, H, HV, K, V = shape.batch, shape.width, shape.h, shape.hv, shape.k, shape.v
+        state = HV * K * V * 4
+        tokens = Bq * Wq
+        nbytes = (Bq * state + tokens * state + tokens * H * K * 2 * 2 + tokens * HV * V * 2 * 2
+                  + tokens * HV * 2 * 2 + tokens * 4)
+        rows[name] = _row(us, nbytes)
+        del g, o
+
+    # a5: the rounded path replay (bf16 pool) and the commit of one accepted node per request, at 1 and 32 requests
+    for Bq in (1, 32):
+        x = records_inputs(Bq, seed=Bq, device=dev)
+        Wq = x["width"]
+        # the path table as the engine derives it: sglang links -> gdn_tree_ancestors (the a2 kernel)
+        links = [tree_links(p, Wq) for p in x["trees"]]
+        nxt_t = torch.tensor([lk[0] for lk in links], dtype=torch.int64, device=dev)
+        sib_t = torch.tensor([lk[1] for lk in links], dtype=torch.int64, device=dev)
+        par_t = torch.empty(Bq, Wq, dtype=torch.int64, device=dev)
+        anc_t = torch.empty(Bq, 3, Wq, dtype=torch.int32, device=dev)
+        paths = torch.zeros(Bq, Wq, 2 + Wq, dtype=torch.int32, device=dev)
+        gdn_tree_ancestors(nxt_t, sib_t, par_t, x["state_indices"], Wq, anc_t, x["query_start_loc"], paths)
+
+        def replay():
+            gdn_tree_records_update(x["A_log"], x["dt_bias"], x["q"], x["k"], x["v"], x["a"], x["b"],
+                                    state=x["state"], state_indices=x["state_indices"],
+                                    query_start_loc=x["query_start_loc"], parent=x["parent"], tree_paths=paths,
+                                    records=x["records"], record_indices=x["record_indices"], width=Wq)
+
+        us = _time_graph(replay, steps)
+        HV, K, V = 48, 128, 128
+        nbytes = (Bq * HV * V * K * 2 + Bq * Wq * 16 * K * 2 * 2 + Bq * Wq * HV * V * 2 * 2 + Bq * Wq * HV * 4
+                  + Bq * Wq * HV * (V + K + 1) * 4)
+        rows[f"a5_path_replay_bf16_b{Bq}"] = _row(us, nbytes)
+        steps_c = torch.full((Bq,), Wq - 1, dtype=torch.int32, device=dev)
+        state5 = x["state"][None]
+        us = _time_graph(lambda: gdn_tree_records_commit(state5, x["records"][None], x["state_indices"],
+                                                         x["record_indices"], steps_c, x["parent"], True), steps)
+        rows[f"a5_commit_bf16_b{Bq}"] = _row(us, Bq * HV * V * K * 2 * 2)
+        del x
+    return rows
+
+
 def _records_chunk(steps: int) -> dict:
     """The records contract's chunk form (one GDN layer's verify writing replay records) at 1 / 4 / 16 / 32 requests:
     the time per call of a HIP graph of 5 calls, best of 3 replays of ``steps`` graphs."""
@@ -125,24 +293,7 @@ def _records_chunk(steps: int) -> dict:
                                   parent=x["parent"], records=x["records"], record_indices=x["record_indices"],
                                   width=x["width"])
 
-        for _ in range(3):
-            call()
-        torch.cuda.synchronize()
-        reps = 5
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                call()
-        best = float("inf")
-        for _ in range(3):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(steps):
-                g.replay()
-            e1.record()
-            e1.synchronize()
-            best = min(best, e0.elapsed_time(e1) * 1e3 / (steps * reps))
-        us[batch] = best
+        us[batch] = _time_graph(call, steps)
         del x, g
     return {"workload": "GDN records chunk form per layer: H16/HV48 K=V=128, 16-node trees, bf16 pool, bf16 q/k/v",
             "us_per_call": us, "reference_published_us": RECORDS_PUBLISHED_US,
@@ -178,6 +329,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the CPU baseline runs whole passes this long")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--records-only", action="store_true", help="time only the records chunk form and print it")
+    ap.add_argument("--rows-only", action="store_true", help="time only the rows outside the step and print them")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -191,6 +343,9 @@ def main() -> int:
         return 0
     if args.records_only:
         print(json.dumps({"records_chunk": _records_chunk(args.steps)}), flush=True)
+        return 0
+    if args.rows_only:
+        print(json.dumps({"rows": _rows(args.steps)}), flush=True)
         return 0
 
     from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
@@ -366,6 +521,7 @@ def main() -> int:
         "cpu_baseline": _cpu_baseline(work, args.cpu_sample, args.cpu_seconds) if work is not None else None,
     }
     result["records_chunk"] = _records_chunk(args.steps)
+    result["rows"] = _rows(args.steps)
     print(json.dumps(result), flush=True)
     return 0
 

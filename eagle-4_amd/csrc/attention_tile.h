@@ -48,6 +48,39 @@ E4_DEV uint4 dequant8(uint2 raw, float scale) {
   return make_uint4(pack(f0[0], f0[1]), pack(f1[0], f1[1]), pack(f2[0], f2[1]), pack(f3[0], f3[1]));
 }
 
+// 8 fp8-e4m3 values (OCP) as 16-bit dtype T, exactly (every e4m3 value is both a bf16 and an fp16 value): four
+// v_cvt_scalef32_pk_* with scale 1.
+template <typename T>
+E4_DEV uint4 widen_fp8x8(uint2 raw) {
+  if constexpr (T::code == EAGLE4_BF16) {
+    return make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.x, 1.0f, false)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.x, 1.0f, true)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.y, 1.0f, false)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.y, 1.0f, true)));
+  } else {
+    return make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw.x, 1.0f, false)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw.x, 1.0f, true)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw.y, 1.0f, false)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(raw.y, 1.0f, true)));
+  }
+}
+
+// A 32-key tile of fp8 K / V pages in LDS (streamed schedule): rows of D bytes, 16-byte chunks XOR-swizzled in their
+// low three index bits per row, so the consumers' 8-byte operand reads fall on distinct banks — K: 16 key rows at one
+// d offset (chunk c of key k at c ^ (k & 7)); V, read transposed (ds_read_b64_tr_b8): 8 key rows, both halves of one
+// chunk (chunk c of key k at c ^ ((k & 3) | (k >> 2 & 4))). Direct loads fill 1 KB runs as for 16-bit tiles.
+template <int D>
+struct Tile8 {
+  static constexpr int CH = D / 16;          // 16-byte chunks per row
+  static constexpr int ROWB = D;             // bytes per row
+  static constexpr int BYTES = kTileKeys * ROWB;
+  static constexpr int RPI = 1024 / ROWB;    // rows one direct-load instruction fills
+  static constexpr int NI = kTileKeys / RPI;  // instructions per matrix per tile
+  static constexpr int SW = CH < 8 ? CH - 1 : 7;
+  static E4_DEV int kswz(int row) { return row & SW; }
+  static E4_DEV int vswz(int row) { return ((row & 3) | ((row >> 2) & 4)) & SW; }
+};
+
 // A 32-key tile of K and of V lives in LDS row-major (rows of D 16-bit values) with its 16-byte chunks XOR-swizzled
 // per row, so both MFMA operand reads are conflict-free: K chunk c of key k sits at c ^ (k & 7); V chunk c at
 // c ^ 2 (k & 3). Direct loads (global_load_lds: lane p of an instruction fills 16-byte slot p of a 1 KB run) fetch
@@ -167,7 +200,7 @@ E4_DEV void store_partial(float* prow, const f32x4_t (&acc)[D / 16], float inv, 
 constexpr int kStreamMaxReqs = 1024;  // per-request query starts and contexts are kept in LDS
 
 struct StreamPlan {
-  int G, row_tiles, C, RG, HR, rows_seg, nwg, direct;
+  int G, row_tiles, C, RG, HR, rows_seg, nwg, direct, fp8;
   int64_t part_off, lse_off;  // float offsets into the workspace (the int64 prefix of tiles per request is first)
 };
 

@@ -1,5 +1,5 @@
-// Tree-verify attention over 16-bit paged KV caches, streamed (vllm/verify_attention.py:29-207 computes the same
-// rows; this is its schedule for gfx950).
+// Tree-verify attention over paged KV caches (16-bit, or fp8-e4m3 with per-(page, KV head) scales), streamed
+// (vllm/verify_attention.py:29-207 computes the same rows; this is its schedule for gfx950).
 //
 // The work is the sequence of 32-key tiles of every segment — (request, KV head, row group), context tiles then
 // draft tiles — in request order. A persistent grid of one workgroup per resident slot takes equal contiguous shares
@@ -151,6 +151,45 @@ E4_DEV OperandOffsets operand_offsets(int g, int l16) {
   return o;
 }
 
+// The same for fp8 context tiles (Tile8): K chunk 2 c + g / 2 (half g & 1) of key row 16 kt + l16 at
+// kb[kt][c & 3] + 128 (c >> 2); the transposing V read of d-tile dt by lane l16 — key row 16 (k / 4) + 4 g + k % 4 with
+// k = l16 / 2, half l16 & 1 — at vb[dt & 7] + 128 (dt >> 3). ds_read_b64_tr_b8 hands lane j of a 16-lane group byte
+// j % 8 of the reads of lanes 2 k + j / 8, k = 0 .. 7: lane l16 then holds d = 16 dt + l16 of keys
+// 16 (k / 4) + 4 g + k % 4, the key order of P^T's operand.
+struct OperandOffsets8 {
+  uint32_t kb[2][4];
+  uint32_t vb[8];
+};
+
+template <int D>
+E4_DEV OperandOffsets8 operand_offsets8(int g, int l16) {
+  using T8 = Tile8<D>;
+  OperandOffsets8 o;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int key = 16 * kt + l16;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o.kb[kt][e] = key * T8::ROWB + 16 * ((2 * e + (g >> 1)) ^ T8::kswz(key)) + 8 * (g & 1);
+  }
+  const int k = l16 >> 1;
+  const int key = 16 * (k >> 2) + 4 * g + (k & 3);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o.vb[e] = key * T8::ROWB + 16 * (e ^ T8::vswz(key)) + 8 * (l16 & 1);
+  return o;
+}
+
+E4_DEV uint2 lds_load8(uint32_t addr) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = *(const __attribute__((address_space(3))) u32x2*)static_cast<uintptr_t>(addr);
+  return make_uint2(v.x, v.y);
+}
+E4_DEV uint2 lds_tr8(uint32_t addr) {
+  typedef int v2i32 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(
+      uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i32*)static_cast<uintptr_t>(addr)));
+}
+
 // Consumer step: one 32-key tile for a wave's 16 rows (lane l16 of each 16-lane group owns row l16; g = lane / 16).
 //   S^T = K Q^T on v_mfma_f32_16x16x32 (s[kt][i]: key 16 kt + 4 g + i of the lane's row); scores outside `vis`
 //   (bit k: key k of the tile is visible to the row) are -inf. Softmax in the log2 domain against a per-row reference
@@ -244,6 +283,89 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 
   }
 }
 
+// The consumer step for an fp8 context tile: the same schedule, operands widened from fp8 as they are read, and the
+// per-(page, KV head) scales folded in per key — into the scores (s_k q . k8) and into P^T (p s_v, whose sum over keys
+// stays the unscaled softmax denominator) — so the products run on the exact e4m3 values. ks[kt] / vs[kt] hold the
+// scales of keys 16 kt + 4 g .. + 3.
+template <int D, typename T>
+E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& off, const uint4 (&q)[D / 32],
+                             f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis, int g,
+                             const float4 (&ks)[2], const float4 (&vs)[2]) {
+  constexpr float kSlack = 16.0f;
+  constexpr int KG = 4, VG = 4;
+  f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int c0 = 0; c0 < D / 32; c0 += KG) {
+    uint2 kraw[2][KG];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
+        const int cc = c0 + c;
+        kraw[kt][c] = lds_load8(kst + off.kb[kt][cc & 3] + 128 * (cc >> 2));
+      }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < KG && c0 + c < D / 32; ++c)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(widen_fp8x8<T>(kraw[kt][c]), q[c0 + c], s[kt]);
+  }
+  auto read_v = [&](int dt) { return lds_tr8(vst + off.vb[dt & 7] + 128 * (dt >> 3)); };
+  uint2 vop[VG];
+#pragma unroll
+  for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);
+  asm volatile("" ::: "memory");
+
+  const uint32_t vv = vis >> (4 * g);
+  const float ksc[2][4] = {{ks[0].x, ks[0].y, ks[0].z, ks[0].w}, {ks[1].x, ks[1].y, ks[1].z, ks[1].w}};
+  const float vsc[2][4] = {{vs[0].x, vs[0].y, vs[0].z, vs[0].w}, {vs[1].x, vs[1].y, vs[1].z, vs[1].w}};
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] * (scale_log2 * ksc[kt][i]) : -INFINITY;
+      s[kt][i] = v;
+      tmax = fmaxf(tmax, v);
+    }
+  if (__any(tmax > mref + kSlack)) {
+    float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
+    const float m_new = fmaxf(mref, rm);
+    const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mref - m_new);
+    mref = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+  }
+  const float ref = mref == -INFINITY ? 0.f : mref;
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4
+    const int kt = p >> 1, i0 = 2 * (p & 1);
+    const float p0 = __builtin_amdgcn_exp2f(s[kt][i0] - ref);
+    const float p1 = __builtin_amdgcn_exp2f(s[kt][i0 + 1] - ref);
+    lsum += p0 + p1;
+    w[p] = pack2<T>(p0 * vsc[kt][i0], p1 * vsc[kt][i0 + 1]);
+  }
+  const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+#pragma unroll
+  for (int d0 = 0; d0 < D / 16; d0 += VG) {
+    uint2 nxt[VG];
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) nxt[i] = read_v(d0 + VG + i);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(widen_fp8x8<T>(vop[i]), pb, acc[d0 + i]);
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) vop[i] = nxt[i];
+    }
+  }
+}
+
 // Visible keys of a tile for one row: context tiles, positions below the context length; draft tiles, draft rows
 // below the width whose ancestor bit the row holds.
 E4_DEV uint32_t visible(bool is_new, int base, int hi, int width, int64_t row_mask) {
@@ -267,10 +389,36 @@ E4_DEV void wait_producer(int later) {
     wait_vm<c0>();
 }
 
+// vmcnt(n) for a count known only at run time (fp8 streams: a context tile and a draft tile issue different numbers
+// of direct loads): a jump over immediate forms.
+#define E4_WAIT_CASE(n) \
+  case n:               \
+    wait_vm<n>();       \
+    break;
+E4_DEV void wait_vm_dyn(int n) {
+  switch (n) {
+    E4_WAIT_CASE(1) E4_WAIT_CASE(2) E4_WAIT_CASE(3) E4_WAIT_CASE(4) E4_WAIT_CASE(5) E4_WAIT_CASE(6) E4_WAIT_CASE(7)
+    E4_WAIT_CASE(8) E4_WAIT_CASE(9) E4_WAIT_CASE(10) E4_WAIT_CASE(11) E4_WAIT_CASE(12) E4_WAIT_CASE(13)
+    E4_WAIT_CASE(14) E4_WAIT_CASE(15) E4_WAIT_CASE(16) E4_WAIT_CASE(17) E4_WAIT_CASE(18) E4_WAIT_CASE(19)
+    E4_WAIT_CASE(20) E4_WAIT_CASE(21) E4_WAIT_CASE(22) E4_WAIT_CASE(23) E4_WAIT_CASE(24) E4_WAIT_CASE(25)
+    E4_WAIT_CASE(26) E4_WAIT_CASE(27) E4_WAIT_CASE(28) E4_WAIT_CASE(29) E4_WAIT_CASE(30) E4_WAIT_CASE(31)
+    E4_WAIT_CASE(32) E4_WAIT_CASE(33) E4_WAIT_CASE(34) E4_WAIT_CASE(35) E4_WAIT_CASE(36) E4_WAIT_CASE(37)
+    E4_WAIT_CASE(38) E4_WAIT_CASE(39) E4_WAIT_CASE(40) E4_WAIT_CASE(41) E4_WAIT_CASE(42) E4_WAIT_CASE(43)
+    E4_WAIT_CASE(44) E4_WAIT_CASE(45) E4_WAIT_CASE(46) E4_WAIT_CASE(47) E4_WAIT_CASE(48) E4_WAIT_CASE(49)
+    E4_WAIT_CASE(50) E4_WAIT_CASE(51) E4_WAIT_CASE(52) E4_WAIT_CASE(53) E4_WAIT_CASE(54) E4_WAIT_CASE(55)
+    E4_WAIT_CASE(56) E4_WAIT_CASE(57) E4_WAIT_CASE(58) E4_WAIT_CASE(59) E4_WAIT_CASE(60) E4_WAIT_CASE(61)
+    E4_WAIT_CASE(62)
+    default:
+      wait_vm<0>();  // 0, and anything the field cannot hold: waiting for everything is always correct
+  }
+}
+#undef E4_WAIT_CASE
+
 constexpr int waves_per_eu(int d) { return d == 256 ? 2 : (d == 128 ? 3 : 4); }
 
 // One workgroup: C consumer waves (16 query rows each) and kProducers producer waves (page lookups, direct loads).
-template <int D, int C, typename T>
+// FP8: context pages are fp8-e4m3 with per-(page, KV head) fp32 scales (draft rows stay 16-bit).
+template <int D, int C, typename T, bool FP8>
 __global__ __launch_bounds__(64 * (C + kProducers)) __attribute__((amdgpu_waves_per_eu(waves_per_eu(D))))
 void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   static_assert(D % 32 == 0 && D >= 32 && D <= 256, "head dim");
@@ -286,6 +434,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   __shared__ int s_ctx[kStreamMaxReqs];
   __shared__ int64_t s_wsum[NW];
   __shared__ int64_t s_start[2];
+  __shared__ __attribute__((aligned(16))) float s_scl[FP8 ? NS : 1][64];  // fp8: K then V scales of a tile's keys
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uni(tid >> 6);
@@ -363,8 +512,9 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     const int page_shift = (page & (page - 1)) == 0 ? __builtin_ctz(page) : -1;
     const char* const kcache = static_cast<const char*>(a.key_cache);
     const char* const vcache = static_cast<const char*>(a.value_cache);
-    const int64_t kb2 = a.stride_kb * 2, ks2 = a.stride_ks * 2, kh2 = a.stride_kh * 2;
-    const int64_t vb2 = a.stride_vb * 2, vs2 = a.stride_vs * 2, vh2 = a.stride_vh * 2;
+    constexpr int EB = FP8 ? 1 : 2;  // bytes per cache element
+    const int64_t kb2 = a.stride_kb * EB, ks2 = a.stride_ks * EB, kh2 = a.stride_kh * EB;
+    const int64_t vb2 = a.stride_vb * EB, vs2 = a.stride_vs * EB, vh2 = a.stride_vh * EB;
     const char* const knew = static_cast<const char*>(a.k_new);
     const char* const vnew = static_cast<const char*>(a.v_new);
     const int64_t knt2 = a.stride_knt * 2, knh2 = a.stride_knh * 2, vnt2 = a.stride_vnt * 2, vnh2 = a.stride_vnh * 2;
@@ -383,6 +533,24 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       voff[i] = static_cast<uint32_t>(slot_row * vs2 + 16 * (pc ^ TL::vswz(r0 + lrow)));
     }
     const uint32_t kbu = static_cast<uint32_t>(kb2), vbu = static_cast<uint32_t>(vb2);
+    // fp8 context tiles: rows of D bytes, instructions nn = pi + kProducers i below Tile8::NI (RPI8 rows each)
+    using T8 = Tile8<D>;
+    constexpr int NG8 = (T8::NI + kProducers - 1) / kProducers;
+    const int pc8 = lane % T8::CH, lrow8 = lane / T8::CH;
+    uint32_t koff8[NG8], voff8[NG8];
+#pragma unroll
+    for (int i = 0; i < NG8; ++i) {
+      const int r0 = (pi + kProducers * i) * T8::RPI;
+      const int slot_row = (whole ? r0 : (r0 & (page - 1))) + lrow8;
+      koff8[i] = static_cast<uint32_t>(slot_row * ks2 + 16 * (pc8 ^ T8::kswz(r0 + lrow8)));
+      voff8[i] = static_cast<uint32_t>(slot_row * vs2 + 16 * (pc8 ^ T8::vswz(r0 + lrow8)));
+    }
+    const int mine8 = (T8::NI - pi + kProducers - 1) / kProducers;  // fp8 instructions of this producer per matrix
+    // the direct loads a tile makes this producer issue (K and V, plus the scales' for producer 0 on fp8 pages)
+    auto loads_of = [&](const Cursor& c) {
+      if (FP8 && c.j < c.n_ctx) return 2 * mine8 + (pi == 0 ? 1 : 0);
+      return 2 * NG;
+    };
 
     // page ids of tile c's keys into ring slot `slot` (draft tiles and look-ahead past the end: a dummy read, so
     // every iteration issues the same loads)
@@ -408,7 +576,47 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
         const int first = page_div(base, page, page_shift);
         const char* const kh = kcache + kvh * kh2;
         const char* const vh = vcache + kvh * vh2;
-        if (p.direct) {
+        if constexpr (FP8) {
+          if (pi == 0) {  // the scales of the tile's keys (K in lanes 0 .. 31, V in 32 .. 63), keys past the context
+                          // take the last one's
+            const int key = lane & 31;
+            const int pos = base + key < c.ctx ? base + key : c.ctx - 1;
+            const int64_t pid = s_pid[slot][page_div(pos, page, page_shift) - first];
+            const float* src = lane < 32 ? a.k_scale + pid * a.stride_ksb + kvh * a.stride_ksh
+                                         : a.v_scale + pid * a.stride_vsb + kvh * a.stride_vsh;
+            dma4(src, uni(lds_addr(s_scl[slot])));
+          }
+          if (p.direct) {
+            const int ids = s_pid[slot][lane];
+            const int in0 = whole ? base - first * page : 0;
+            const char* const kt = kh + in0 * ks2;
+            const char* const vt = vh + in0 * vs2;
+#pragma unroll
+            for (int i = 0; i < NG8; ++i) {
+              const int nn = pi + kProducers * i;
+              if (nn < T8::NI) {
+                const int rel = whole ? 0 : (nn * T8::RPI) >> page_shift;
+                const uint32_t pid = static_cast<uint32_t>(__builtin_amdgcn_readlane(ids, rel));
+                dma16s(kt + static_cast<uint64_t>(pid) * kbu, koff8[i], uni(kl + nn * 1024));
+                dma16s(vt + static_cast<uint64_t>(pid) * vbu, voff8[i], uni(vl + nn * 1024));
+              }
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < NG8; ++i) {
+              const int nn = pi + kProducers * i;
+              if (nn < T8::NI) {
+                const int row = nn * T8::RPI + lrow8;
+                const int pos = base + row < c.ctx ? base + row : c.ctx - 1;
+                const int pg = page_div(pos, page, page_shift);
+                const int64_t pid = s_pid[slot][pg - first];
+                const int64_t sl = pos - pg * page;
+                dma16(kh + pid * kb2 + sl * ks2 + 16 * (pc8 ^ T8::kswz(row)), uni(kl + nn * 1024));
+                dma16(vh + pid * vb2 + sl * vs2 + 16 * (pc8 ^ T8::vswz(row)), uni(vl + nn * 1024));
+              }
+            }
+          }
+        } else if (p.direct) {
           // a row group lies in one page (rows past the context read the last page's slots: in bounds, masked); the
           // tile's page ids come from one LDS read, lane i holding the id of page first + i
           const int ids = s_pid[slot][lane];
@@ -463,8 +671,16 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     }
     wait_vm<0>();
     __syncthreads();
+    static_assert(NS == 4, "the load-count window below is written for four stages");
+    int n1 = 0, n2 = 0;  // fp8: direct loads of tiles x + 1 and x + 2 (tiles differ: fp8 context, 16-bit draft)
     for (int i = 0; i < NS - 1; ++i) {
-      if (g0 + i < g1) load_tile(cd, static_cast<int>((g0 + i) & (NS - 1)));
+      int n = 0;
+      if (g0 + i < g1) {
+        n = loads_of(cd);
+        load_tile(cd, static_cast<int>((g0 + i) & (NS - 1)));
+      }
+      if (i == 1) n1 = n;
+      if (i == 2) n2 = n;
       cur_next(cd, s_qsl, s_ctx, B, HR);
       lookup(cl, static_cast<int>((g0 + NS - 1 + i) & (NS - 1)));
       cur_next(cl, s_qsl, s_ctx, B, HR);
@@ -474,12 +690,21 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       const int slot = static_cast<int>(x & (NS - 1));
       const int64_t left = g1 - x - 1;
       const int later = static_cast<int>(left < NS - 2 ? left : NS - 2);
-      if (pi == 0)
+      if constexpr (FP8) {  // loads issued after tile x's: those of the later tiles and the lookups 4, 5 ahead
+        wait_vm_dyn((later >= 1 ? n1 : 0) + (later >= 2 ? n2 : 0) + (pi == 0 ? NS - 2 : 0));
+      } else if (pi == 0) {
         wait_producer<NS, 2 * NG, 1>(later);
-      else
+      } else {
         wait_producer<NS, 2 * NG, 0>(later);
+      }
       __syncthreads();  // tile x is in LDS; stage x - 1 has been read by every consumer
-      if (x + NS - 1 < g1) load_tile(cd, (slot + NS - 1) & (NS - 1));
+      int n3 = 0;
+      if (x + NS - 1 < g1) {
+        n3 = loads_of(cd);
+        load_tile(cd, (slot + NS - 1) & (NS - 1));
+      }
+      n1 = n2;
+      n2 = n3;
       cur_next(cd, s_qsl, s_ctx, B, HR);
       lookup(cl, (slot + 2 * NS - 2) & (NS - 1));
       cur_next(cl, s_qsl, s_ctx, B, HR);
@@ -518,6 +743,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   };
   reset();
   const OperandOffsets off = operand_offsets<D>(g, l16);
+  OperandOffsets8 off8 = {};
+  if constexpr (FP8) off8 = operand_offsets8<D>(g, l16);
   int piece_j0 = cc.j;
   const int rows_seg = p.rows_seg;
 #pragma unroll
@@ -528,8 +755,15 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     __syncthreads();
     const bool is_new = cc.j >= cc.n_ctx;
     const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * kTileKeys;
-    consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
-                       visible(is_new, base, cc.ctx, cc.width, row_mask), g);
+    const uint32_t vis = visible(is_new, base, cc.ctx, cc.width, row_mask);
+    if (FP8 && !is_new) {
+      const float4* sc = reinterpret_cast<const float4*>(s_scl[FP8 ? slot : 0]);
+      const float4 ks[2] = {sc[g], sc[4 + g]}, vs[2] = {sc[8 + g], sc[12 + g]};
+      consume_tile_fp8<D, T>(lds_addr(smem[slot][0]), lds_addr(smem[slot][1]), off8, q, acc, mref, lsum, scale_log2,
+                             vis, g, ks, vs);
+    } else {
+      consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2, vis, g);
+    }
 
     const bool seg_end = cc.j == cc.tiles - 1;
     if (seg_end || x == g1 - 1) {
@@ -612,12 +846,13 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
                             (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d) = o;
 }
 
-template <int D, int C, typename T>
+template <int D, int C, typename T, bool FP8>
 int resident_groups() {
   static const int per_cu = [] {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(verify_stream_kernel<D, C, T>),
-                                                     64 * (C + kProducers), 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(verify_stream_kernel<D, C, T, FP8>), 64 * (C + kProducers), 0) !=
+        hipSuccess)
       n = 0;
     return n;
   }();
@@ -628,49 +863,57 @@ int resident_groups() {
   return per_cu * cus;
 }
 
-// consumer counts instantiated: 2, 4 and 6 waves (a group of row tiles takes the smallest that holds it)
-template <int D, typename T>
-int groups_c(int c) {
-  switch (c) {
-    case 2: return resident_groups<D, 2, T>();
-    case 4: return resident_groups<D, 4, T>();
-    default: return resident_groups<D, 6, T>();
-  }
-}
-
-int groups(const eagle4_attn_args& a, int c) {
-  const bool bf = a.dtype == EAGLE4_BF16;
-  switch (a.D) {
-    case 32: return bf ? groups_c<32, e4::Bf16>(c) : groups_c<32, e4::F16>(c);
-    case 64: return bf ? groups_c<64, e4::Bf16>(c) : groups_c<64, e4::F16>(c);
-    case 128: return bf ? groups_c<128, e4::Bf16>(c) : groups_c<128, e4::F16>(c);
-    default: return bf ? groups_c<256, e4::Bf16>(c) : groups_c<256, e4::F16>(c);
-  }
-}
-
-template <int D, int C, typename T>
+template <int D, int C, typename T, bool FP8>
 int launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
-  verify_stream_kernel<D, C, T><<<p.nwg, 64 * (C + kProducers), 0, s>>>(a, p);
+  verify_stream_kernel<D, C, T, FP8><<<p.nwg, 64 * (C + kProducers), 0, s>>>(a, p);
   verify_stream_merge<D, T><<<dim3(a.num_reqs * p.HR, e4::ceil_div(static_cast<int64_t>(p.rows_seg) * (D / 4), 256)), 256, 0,
                                s>>>(a, p);
   return E4_LAUNCH_STATUS();
 }
 
-template <int D, typename T>
-int launch_c(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
-  switch (p.C) {
-    case 2: return launch<D, 2, T>(a, p, s);
-    case 4: return launch<D, 4, T>(a, p, s);
-    default: return launch<D, 6, T>(a, p, s);
+// The instantiations: head dims 32 .. 256, 2 / 4 / 6 consumer waves (a group of row tiles takes the smallest that
+// holds it), bf16 / fp16 rows, 16-bit or fp8 pages; `go` receives the one the call needs (as a type tag).
+template <int D_, int C_, typename T_, bool FP8_>
+struct Config {
+  static constexpr int D = D_, C = C_;
+  using T = T_;
+  static constexpr bool FP8 = FP8_;
+};
+
+template <int D, typename T, bool FP8, typename F>
+int with_c(int c, F&& go) {
+  switch (c) {
+    case 2: return go(Config<D, 2, T, FP8>{});
+    case 4: return go(Config<D, 4, T, FP8>{});
+    default: return go(Config<D, 6, T, FP8>{});
+  }
+}
+
+template <int D, typename F>
+int with_t(const eagle4_attn_args& a, int c, F&& go) {
+  const bool bf = a.dtype == EAGLE4_BF16, f8 = a.cache_dtype == EAGLE4_FP8_E4M3;
+  if (bf) return f8 ? with_c<D, e4::Bf16, true>(c, go) : with_c<D, e4::Bf16, false>(c, go);
+  return f8 ? with_c<D, e4::F16, true>(c, go) : with_c<D, e4::F16, false>(c, go);
+}
+
+template <typename F>
+int with_config(const eagle4_attn_args& a, int c, F&& go) {
+  switch (a.D) {
+    case 32: return with_t<32>(a, c, go);
+    case 64: return with_t<64>(a, c, go);
+    case 128: return with_t<128>(a, c, go);
+    default: return with_t<256>(a, c, go);
   }
 }
 
 }  // namespace
 
-// 16-bit caches (the same dtype as q) and at most kStreamMaxReqs requests; the rest of the contract is checked by
-// the caller.
+// 16-bit caches of q's dtype, or fp8-e4m3 caches with their scales; at most kStreamMaxReqs requests; the library's
+// context split (a caller-chosen split size selects the split-context schedule). The rest of the contract is checked
+// by the caller.
 bool stream_covered(const eagle4_attn_args& a) {
-  return a.cache_dtype == a.dtype && a.num_reqs <= kStreamMaxReqs;
+  const bool fp8 = a.cache_dtype == EAGLE4_FP8_E4M3 && a.k_scale != nullptr && a.v_scale != nullptr;
+  return (a.cache_dtype == a.dtype || fp8) && a.num_reqs <= kStreamMaxReqs && a.chunk <= 0;
 }
 
 bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
@@ -681,15 +924,20 @@ bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
   p.C = need <= 2 ? 2 : (need <= 4 ? 4 : 6);
   p.HR = a.Hkv * p.RG;
   p.rows_seg = 16 * p.C;
-  // direct page addressing: every direct-load instruction's rows (1024 / (2 D) consecutive keys) in one page, a
-  // page's slots addressable by 32-bit lane offsets, block strides below 4 GB
-  const int rpi = 512 / a.D;
+  p.fp8 = a.cache_dtype == EAGLE4_FP8_E4M3;
+  // direct page addressing: every direct-load instruction's rows (1024 / (element bytes x D) consecutive keys) in one
+  // page, a page's slots addressable by 32-bit lane offsets, block strides below 4 GB
+  const int eb = p.fp8 ? 1 : 2;
+  const int rpi = 1024 / (eb * a.D);
   const bool aligned = a.page % kTileKeys == 0 || (kTileKeys % a.page == 0 && a.page >= rpi);
-  const int64_t span = static_cast<int64_t>(a.page) * (a.stride_ks > a.stride_vs ? a.stride_ks : a.stride_vs) * 2;
-  const int64_t block_bytes = 2 * (a.stride_kb > a.stride_vb ? a.stride_kb : a.stride_vb);
+  const int64_t span = static_cast<int64_t>(a.page) * (a.stride_ks > a.stride_vs ? a.stride_ks : a.stride_vs) * eb;
+  const int64_t block_bytes = eb * (a.stride_kb > a.stride_vb ? a.stride_kb : a.stride_vb);
   p.direct = aligned && a.stride_ks >= 0 && a.stride_vs >= 0 && a.stride_kb >= 0 && a.stride_vb >= 0 &&
              span < (int64_t(1) << 31) && block_bytes < (int64_t(1) << 32);
-  p.nwg = groups(a, p.C);
+  p.nwg = with_config(a, p.C, [](auto cfg) {
+    using K = decltype(cfg);
+    return resident_groups<K::D, K::C, typename K::T, K::FP8>();
+  });
   if (p.nwg <= 0) return false;
   const int64_t slots = static_cast<int64_t>(a.num_reqs) * p.HR + p.nwg;
   const int64_t rows_seg = p.rows_seg;
@@ -704,13 +952,10 @@ int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args& a) {
 }
 
 int stream_launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
-  const bool bf = a.dtype == EAGLE4_BF16;
-  switch (a.D) {
-    case 32: return bf ? launch_c<32, e4::Bf16>(a, p, s) : launch_c<32, e4::F16>(a, p, s);
-    case 64: return bf ? launch_c<64, e4::Bf16>(a, p, s) : launch_c<64, e4::F16>(a, p, s);
-    case 128: return bf ? launch_c<128, e4::Bf16>(a, p, s) : launch_c<128, e4::F16>(a, p, s);
-    default: return bf ? launch_c<256, e4::Bf16>(a, p, s) : launch_c<256, e4::F16>(a, p, s);
-  }
+  return with_config(a, p.C, [&](auto cfg) {
+    using K = decltype(cfg);
+    return launch<K::D, K::C, typename K::T, K::FP8>(a, p, s);
+  });
 }
 
 }  // namespace e4attn

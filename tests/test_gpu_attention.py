@@ -89,6 +89,34 @@ def test_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, page, 
         assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))  # rows past the batch untouched
 
 
+@pytest.mark.parametrize(
+    "contexts, parents, heads, kv_heads, d, page",
+    [
+        ([300], [[-1, 0, 0, 1, 1, 2, 3]], 6, 1, 64, 16),
+        ([5, 700, 0], [[-1, 0, 1], [-1, 0, 0, 1, 2, 2, 3, 4, 5], [-1, 0]], 4, 2, 32, 32),
+        ([1500, 2], [[-1, 0, 0, 1], [-1, 0]], 8, 2, 128, 16),
+        ([1000], [[-1, 0, 1, 1, 3, 0]], 12, 2, 256, 48),  # a page size that is not a power of two
+        ([777, 64], [[-1, 0, 0, 2], [-1, 0, 1]], 6, 2, 256, 2),  # pages smaller than a load instruction's rows
+    ],
+)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp8_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, page, dtype):
+    """fp8-e4m3 pages (per-(page, KV head) scales) on both schedules: the streamed one (the library's split) and the
+    split-context one (a caller-chosen split of 64 or 256 keys)."""
+    from workloads import _quantize_fp8_pages
+
+    announce(f"attention fp8 contexts={contexts} heads={heads}/{kv_heads} d={d} page={page} {dtype}")
+    inp = _inputs(contexts, parents, heads, kv_heads, d, page, dtype, seed=len(contexts) * 100 + heads + 7)
+    inp["key_cache"], inp["k_scale"] = _quantize_fp8_pages(inp["key_cache"].float() * 3.0)
+    inp["value_cache"], inp["v_scale"] = _quantize_fp8_pages(inp["value_cache"].float() * 0.5)
+    tokens = sum(len(p) for p in parents)
+    want = _want(inp, fp8=True)
+    for chunk in (0, 64, 256):
+        got = _run(dev, inp, dtype, chunk=chunk, fp8=True)
+        _close(got[:tokens], want[:tokens])
+        assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))
+
+
 def test_b1_l512_workload(dev):
     """Batch 1, 16 seeded nodes, prefix 512, 16 / 4 heads, D 128 (the oracle's fp32 CPU case, run in bf16)."""
     announce("attention b1 l512")
@@ -115,10 +143,11 @@ def test_fp8_pages_match_dequantized_oracle(dev, chunk):
     _close(_run(dev, inp, torch.bfloat16, chunk=chunk, fp8=True), _want(inp, fp8=True))
 
 
-def test_fp8_dequant_is_ocp_e4m3(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fp8_dequant_is_ocp_e4m3(dev, dtype):
     """Every one of the 256 fp8 codes dequantizes as torch's float8_e4m3fn (OCP): one page whose keys and values
-    are the codes, attended by a single row with a one-hot query, reads them back exactly (bf16 outputs)."""
-    announce("attention fp8 code table")
+    are the codes, attended by a single row with a one-hot query, reads them back exactly (16-bit outputs)."""
+    announce(f"attention fp8 code table {dtype}")
     d, page = 64, 16
     codes = torch.arange(256, dtype=torch.uint8)
     codes = codes[(codes & 0x7F) != 0x7F]  # NaN codes stay out
@@ -138,16 +167,16 @@ def test_fp8_dequant_is_ocp_e4m3(dev):
         kc = torch.zeros(pages * page, d)
         kc[kpos, 0] = 448.0
         key_cache = kc.to(torch.float8_e4m3fn).view(pages, page, 1, d)
-        q = torch.zeros(1, 1, d, dtype=torch.bfloat16)
+        q = torch.zeros(1, 1, d, dtype=dtype)
         q[0, 0, 0] = 1.0
-        out = torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev)
-        verify_attention(q.to(dev), torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev),
-                         torch.zeros(1, 1, d, dtype=torch.bfloat16, device=dev), key_cache.to(dev), value.to(dev),
+        out = torch.zeros(1, 1, d, dtype=dtype, device=dev)
+        verify_attention(q.to(dev), torch.zeros(1, 1, d, dtype=dtype, device=dev),
+                         torch.zeros(1, 1, d, dtype=dtype, device=dev), key_cache.to(dev), value.to(dev),
                          torch.arange(pages, dtype=torch.int32, device=dev)[None], torch.tensor([keys], dtype=torch.int32, device=dev),
                          torch.tensor([0, 1], dtype=torch.int32, device=dev), torch.ones(1, 1, dtype=torch.int64, device=dev),
                          1.0, out, max_query_len=1, k_scale=scale.to(dev), v_scale=scale.to(dev))
         torch.cuda.synchronize()
-        torch.testing.assert_close(out[0, 0].cpu().float(), want_vals[kpos].to(torch.bfloat16).float(), atol=0, rtol=0)
+        torch.testing.assert_close(out[0, 0].cpu().float(), want_vals[kpos].to(dtype).float(), atol=0, rtol=0)
 
 
 def test_ragged_batch_with_empty_requests(dev):

@@ -67,6 +67,21 @@ def window_codes(parents: list[int]) -> list[list[int]]:
     return anc
 
 
+def tree_links(parents: list[int], width: int) -> tuple[list[int], list[int]]:
+    """First-child / next-sibling links of a parent-first tree (children in row order; sglang's form), -1 padded."""
+    first = [-1] * width
+    sibling = [-1] * width
+    last: dict[int, int] = {}
+    for node in range(1, len(parents)):
+        p = parents[node]
+        if p in last:
+            sibling[last[p]] = node
+        else:
+            first[p] = node
+        last[p] = node
+    return first, sibling
+
+
 def root_path(parents: list[int], node: int) -> list[int]:
     path = []
     while node >= 0:
