@@ -65,17 +65,20 @@ E4_DEV uint4 widen_fp8x8(uint2 raw) {
   }
 }
 
-// A 32-key tile of fp8 K / V pages in LDS (streamed schedule): rows of D bytes, 16-byte chunks XOR-swizzled in their
-// low three index bits per row, so the consumers' 8-byte operand reads fall on distinct banks — K: 16 key rows at one
-// d offset (chunk c of key k at c ^ (k & 7)); V, read transposed (ds_read_b64_tr_b8): 8 key rows, both halves of one
-// chunk (chunk c of key k at c ^ ((k & 3) | (k >> 2 & 4))). Direct loads fill 1 KB runs as for 16-bit tiles.
+// A context tile of fp8 K / V pages in LDS (streamed schedule): 64 keys, so that it fills the bytes of a 32-key
+// 16-bit tile; rows of D bytes, 16-byte chunks XOR-swizzled in their low three index bits per row, so the consumers'
+// 8-byte operand reads fall on distinct banks — K: 16 key rows at one d offset (chunk c of key k at c ^ (k & 7)); V,
+// read transposed (ds_read_b64_tr_b8): 8 key rows, both halves of one chunk (chunk c of key k at
+// c ^ ((k & 3) | (k >> 2 & 4))). Both swizzles repeat every 32 rows. Direct loads fill 1 KB runs as for 16-bit tiles.
+constexpr int kTileKeys8 = 64;
+
 template <int D>
 struct Tile8 {
   static constexpr int CH = D / 16;          // 16-byte chunks per row
   static constexpr int ROWB = D;             // bytes per row
-  static constexpr int BYTES = kTileKeys * ROWB;
+  static constexpr int BYTES = kTileKeys8 * ROWB;
   static constexpr int RPI = 1024 / ROWB;    // rows one direct-load instruction fills
-  static constexpr int NI = kTileKeys / RPI;  // instructions per matrix per tile
+  static constexpr int NI = kTileKeys8 / RPI;  // instructions per matrix per tile
   static constexpr int SW = CH < 8 ? CH - 1 : 7;
   static E4_DEV int kswz(int row) { return row & SW; }
   static E4_DEV int vswz(int row) { return ((row & 3) | ((row >> 2) & 4)) & SW; }

@@ -67,6 +67,8 @@ struct Cursor {
   int tiles, n_ctx, ctx, qs, width;
 };
 
+// CK: keys of a context tile (32 for 16-bit pages, 64 for fp8); draft tiles hold 32 keys.
+template <int CK>
 E4_DEV void cur_load(Cursor& c, const int* s_qsl, const int* s_ctx, int B) {
   if (c.b >= B) {  // past the last request (a look-ahead cursor): an empty draft tile
     c.tiles = 1;
@@ -80,10 +82,11 @@ E4_DEV void cur_load(Cursor& c, const int* s_qsl, const int* s_ctx, int B) {
   const int w = uni(s_qsl[c.b + 1]) - c.qs;
   c.width = w < 64 ? w : 64;
   c.ctx = uni(s_ctx[c.b]);
-  c.n_ctx = c.width > 0 ? (c.ctx + kTileKeys - 1) / kTileKeys : 0;
+  c.n_ctx = c.width > 0 ? (c.ctx + CK - 1) / CK : 0;
   c.tiles = c.width > 0 ? c.n_ctx + (c.width + kTileKeys - 1) / kTileKeys : 0;
 }
 
+template <int CK>
 E4_DEV void cur_next(Cursor& c, const int* s_qsl, const int* s_ctx, int B, int HR) {
   if (++c.j < c.tiles) return;
   c.j = 0;
@@ -91,15 +94,16 @@ E4_DEV void cur_next(Cursor& c, const int* s_qsl, const int* s_ctx, int B, int H
   c.k = 0;
   do {
     ++c.b;
-    cur_load(c, s_qsl, s_ctx, B);
+    cur_load<CK>(c, s_qsl, s_ctx, B);
   } while (c.tiles == 0);
 }
 
+template <int CK>
 E4_DEV int tiles_of(const int* s_qsl, const int* s_ctx, int b) {
   const int w = s_qsl[b + 1] - s_qsl[b];
   if (w <= 0) return 0;
   const int wk = w < 64 ? w : 64;
-  return (s_ctx[b] + kTileKeys - 1) / kTileKeys + (wk + kTileKeys - 1) / kTileKeys;
+  return (s_ctx[b] + CK - 1) / CK + (wk + kTileKeys - 1) / kTileKeys;
 }
 
 E4_DEV int64_t active_groups(int64_t tiles_all, int nwg) {
@@ -427,6 +431,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   constexpr int NT = 64 * NW;
   constexpr int NS = kStages;
   constexpr int NG = TL::NI / kProducers;  // row groups per producer: nn = producer + kProducers i, K then V
+  constexpr int CK = FP8 ? kTileKeys8 : kTileKeys;  // keys of a context tile
   static_assert(TL::NI % kProducers == 0, "row groups split evenly");
   __shared__ __attribute__((aligned(1024))) char smem[NS][2][TL::BYTES];  // [stage][K, V]
   __shared__ __attribute__((aligned(256))) int s_pid[NS][64];             // page ids of a tile's keys
@@ -434,7 +439,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   __shared__ int s_ctx[kStreamMaxReqs];
   __shared__ int64_t s_wsum[NW];
   __shared__ int64_t s_start[2];
-  __shared__ __attribute__((aligned(16))) float s_scl[FP8 ? NS : 1][64];  // fp8: K then V scales of a tile's keys
+  __shared__ __attribute__((aligned(16))) float s_scl[FP8 ? NS : 1][2 * kTileKeys8];  // fp8: K, V scales per key
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uni(tid >> 6);
@@ -456,7 +461,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   const int b_lo = tid * per < B ? tid * per : B;
   const int b_hi = b_lo + per < B ? b_lo + per : B;
   int64_t mine = 0;
-  for (int b = b_lo; b < b_hi; ++b) mine += tiles_of(s_qsl, s_ctx, b);
+  for (int b = b_lo; b < b_hi; ++b) mine += tiles_of<CK>(s_qsl, s_ctx, b);
   int64_t incl = mine;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -481,7 +486,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     int64_t* pre = reinterpret_cast<int64_t*>(a.workspace);
     int64_t run = before;
     for (int b = b_lo; b < b_hi; ++b) {
-      const int tb = tiles_of(s_qsl, s_ctx, b);
+      const int tb = tiles_of<CK>(s_qsl, s_ctx, b);
       if (w == 0) pre[b] = run;
       if (tb > 0 && run * HR <= g0 && g0 < (run + tb) * HR) {
         s_start[0] = b;
@@ -498,7 +503,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   Cursor cc;
   {
     cc.b = uni(static_cast<int>(s_start[0]));
-    cur_load(cc, s_qsl, s_ctx, B);
+    cur_load<CK>(cc, s_qsl, s_ctx, B);
     const int64_t off = g0 - s_start[1] * HR;
     cc.k = uni(static_cast<int>(off / cc.tiles));
     cc.j = uni(static_cast<int>(off - static_cast<int64_t>(cc.k) * cc.tiles));
@@ -522,8 +527,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     const int32_t* const bt_dummy = static_cast<const int32_t*>(a.query_start_loc.ptr);  // any readable word
     const int pc = lane % TL::CH, lrow = lane / TL::CH;
     // direct pages: lane offsets of this producer's row group i (nn = pi + kProducers i) from the start of its page
-    // (pages of 32 keys or more hold the whole tile: the tile's first slot is added to the page base instead)
-    const bool whole = page >= kTileKeys;
+    // (pages that are multiples of the context tile hold the whole tile: its first slot is added to the page base)
+    const bool whole = page % CK == 0;
     uint32_t koff[NG], voff[NG];
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
@@ -548,7 +553,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     const int mine8 = (T8::NI - pi + kProducers - 1) / kProducers;  // fp8 instructions of this producer per matrix
     // the direct loads a tile makes this producer issue (K and V, plus the scales' for producer 0 on fp8 pages)
     auto loads_of = [&](const Cursor& c) {
-      if (FP8 && c.j < c.n_ctx) return 2 * mine8 + (pi == 0 ? 1 : 0);
+      if (FP8 && c.j < c.n_ctx) return 2 * mine8 + (pi == 0 ? 2 : 0);
       return 2 * NG;
     };
 
@@ -558,9 +563,9 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       if (pi != 0) return;
       const int32_t* src = bt_dummy;
       if (c.j < c.n_ctx) {
-        const int base = c.j * kTileKeys;
+        const int base = c.j * CK;
         const int first = page_div(base, page, page_shift);
-        const int last = page_div(base + kTileKeys - 1 < c.ctx ? base + kTileKeys - 1 : c.ctx - 1, page, page_shift);
+        const int last = page_div(base + CK - 1 < c.ctx ? base + CK - 1 : c.ctx - 1, page, page_shift);
         const int idx = first + lane < last ? first + lane : last;
         src = bt + static_cast<int64_t>(c.b) * a.block_table.s0 + idx;
       }
@@ -572,19 +577,16 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       const int kvh = c.k / RG;
       const uint32_t kl = lds_addr(smem[slot][0]), vl = lds_addr(smem[slot][1]);
       if (c.j < c.n_ctx) {
-        const int base = c.j * kTileKeys;
+        const int base = c.j * CK;
         const int first = page_div(base, page, page_shift);
         const char* const kh = kcache + kvh * kh2;
         const char* const vh = vcache + kvh * vh2;
         if constexpr (FP8) {
-          if (pi == 0) {  // the scales of the tile's keys (K in lanes 0 .. 31, V in 32 .. 63), keys past the context
-                          // take the last one's
-            const int key = lane & 31;
-            const int pos = base + key < c.ctx ? base + key : c.ctx - 1;
+          if (pi == 0) {  // the scales of the tile's 64 keys, K then V (keys past the context take the last one's)
+            const int pos = base + lane < c.ctx ? base + lane : c.ctx - 1;
             const int64_t pid = s_pid[slot][page_div(pos, page, page_shift) - first];
-            const float* src = lane < 32 ? a.k_scale + pid * a.stride_ksb + kvh * a.stride_ksh
-                                         : a.v_scale + pid * a.stride_vsb + kvh * a.stride_vsh;
-            dma4(src, uni(lds_addr(s_scl[slot])));
+            dma4(a.k_scale + pid * a.stride_ksb + kvh * a.stride_ksh, uni(lds_addr(s_scl[slot])));
+            dma4(a.v_scale + pid * a.stride_vsb + kvh * a.stride_vsh, uni(lds_addr(s_scl[slot] + 64)));
           }
           if (p.direct) {
             const int ids = s_pid[slot][lane];
@@ -667,7 +669,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     // barrier after each step (a lookup reuses the ring slot that both producers read in the step before)
     for (int i = 0; i < NS - 1; ++i) {
       lookup(cl, static_cast<int>((g0 + i) & (NS - 1)));
-      cur_next(cl, s_qsl, s_ctx, B, HR);
+      cur_next<CK>(cl, s_qsl, s_ctx, B, HR);
     }
     wait_vm<0>();
     __syncthreads();
@@ -681,9 +683,9 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       }
       if (i == 1) n1 = n;
       if (i == 2) n2 = n;
-      cur_next(cd, s_qsl, s_ctx, B, HR);
+      cur_next<CK>(cd, s_qsl, s_ctx, B, HR);
       lookup(cl, static_cast<int>((g0 + NS - 1 + i) & (NS - 1)));
-      cur_next(cl, s_qsl, s_ctx, B, HR);
+      cur_next<CK>(cl, s_qsl, s_ctx, B, HR);
       __syncthreads();
     }
     for (int64_t x = g0; x < g1; ++x) {
@@ -705,9 +707,9 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       }
       n1 = n2;
       n2 = n3;
-      cur_next(cd, s_qsl, s_ctx, B, HR);
+      cur_next<CK>(cd, s_qsl, s_ctx, B, HR);
       lookup(cl, (slot + 2 * NS - 2) & (NS - 1));
-      cur_next(cl, s_qsl, s_ctx, B, HR);
+      cur_next<CK>(cl, s_qsl, s_ctx, B, HR);
     }
     wait_vm<0>();
     return;
@@ -754,15 +756,19 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     const int slot = static_cast<int>(x & (NS - 1));
     __syncthreads();
     const bool is_new = cc.j >= cc.n_ctx;
-    const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * kTileKeys;
-    const uint32_t vis = visible(is_new, base, cc.ctx, cc.width, row_mask);
-    if (FP8 && !is_new) {
+    const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * CK;
+    if (FP8 && !is_new) {  // two 32-key halves of the 64-key fp8 tile
       const float4* sc = reinterpret_cast<const float4*>(s_scl[FP8 ? slot : 0]);
-      const float4 ks[2] = {sc[g], sc[4 + g]}, vs[2] = {sc[8 + g], sc[12 + g]};
-      consume_tile_fp8<D, T>(lds_addr(smem[slot][0]), lds_addr(smem[slot][1]), off8, q, acc, mref, lsum, scale_log2,
-                             vis, g, ks, vs);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 ks[2] = {sc[8 * h + g], sc[8 * h + 4 + g]}, vs[2] = {sc[16 + 8 * h + g], sc[16 + 8 * h + 4 + g]};
+        consume_tile_fp8<D, T>(lds_addr(smem[slot][0]) + 32 * h * D, lds_addr(smem[slot][1]) + 32 * h * D, off8, q,
+                               acc, mref, lsum, scale_log2, visible(false, base + 32 * h, cc.ctx, cc.width, row_mask),
+                               g, ks, vs);
+      }
     } else {
-      consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2, vis, g);
+      consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
+                         visible(is_new, base, cc.ctx, cc.width, row_mask), g);
     }
 
     const bool seg_end = cc.j == cc.tiles - 1;
@@ -781,7 +787,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
         }
       }
       if (x + 1 < g1) {
-        cur_next(cc, s_qsl, s_ctx, B, HR);
+        cur_next<CK>(cc, s_qsl, s_ctx, B, HR);
         enter(cc);
         reset();
         piece_j0 = 0;
@@ -929,7 +935,8 @@ bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
   // page, a page's slots addressable by 32-bit lane offsets, block strides below 4 GB
   const int eb = p.fp8 ? 1 : 2;
   const int rpi = 1024 / (eb * a.D);
-  const bool aligned = a.page % kTileKeys == 0 || (kTileKeys % a.page == 0 && a.page >= rpi);
+  const int ck = p.fp8 ? kTileKeys8 : kTileKeys;
+  const bool aligned = a.page % ck == 0 || (ck % a.page == 0 && a.page >= rpi);
   const int64_t span = static_cast<int64_t>(a.page) * (a.stride_ks > a.stride_vs ? a.stride_ks : a.stride_vs) * eb;
   const int64_t block_bytes = eb * (a.stride_kb > a.stride_vb ? a.stride_kb : a.stride_vb);
   p.direct = aligned && a.stride_ks >= 0 && a.stride_vs >= 0 && a.stride_kb >= 0 && a.stride_vb >= 0 &&
