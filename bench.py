@@ -142,8 +142,8 @@ def _row(us: float, nbytes: int | None = None, **extra) -> dict:
 def _rows(steps: int) -> dict:
     """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
     batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
-    attention at batch 512, the GDN walk at batch 1 and 256, 16-bit attention at batch 1, and the rounded records path
-    replay and commit. Algorithmic bytes count every element once."""
+    attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, and the rounded records
+    path replay and commit. Algorithmic bytes count every element once."""
     import math
 
     import numpy as np
@@ -199,9 +199,10 @@ def _rows(steps: int) -> dict:
     rows["a8_tail_words_w16"] = _row(us)
 
     # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
-    for name, shape, fp8 in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True),
-                             ("a6_attention_bf16_b1_d128", ATTN_B1, False)):
-        x = attention_inputs(shape, seed=3, device=dev, fp8=fp8, gen_device=dev)
+    for name, shape, fp8, dtype in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True, torch.bfloat16),
+                                    ("a6_attention_fp32_b1_d128", ATTN_B1, False, torch.float32),
+                                    ("a6_attention_bf16_b1_d128", ATTN_B1, False, torch.bfloat16)):
+        x = attention_inputs(shape, seed=3, device=dev, dtype=dtype, fp8=fp8, gen_device=dev)
         out = torch.empty_like(x["q"])
         kw = dict(k_scale=x["k_scale"], v_scale=x["v_scale"]) if fp8 else {}
 
@@ -213,9 +214,10 @@ def _rows(steps: int) -> dict:
         us = _time_graph(attn, steps)
         ctx = x["context_lens"].tolist()
         tokens = shape.batch * shape.width
-        esz = 1 if fp8 else 2
-        nbytes = (sum(ctx) * shape.hkv * shape.d * 2 * esz + tokens * shape.hq * shape.d * 2 * 2
-                  + tokens * shape.hkv * shape.d * 2 * 2 + sum(math.ceil(L / shape.page) for L in ctx) * 4
+        esz = 1 if fp8 else x["key_cache"].element_size()
+        qsz = x["q"].element_size()
+        nbytes = (sum(ctx) * shape.hkv * shape.d * 2 * esz + tokens * shape.hq * shape.d * 2 * qsz
+                  + tokens * shape.hkv * shape.d * 2 * qsz + sum(math.ceil(L / shape.page) for L in ctx) * 4
                   + (sum(math.ceil(L / shape.page) for L in ctx) * shape.hkv * 4 * 2 if fp8 else 0))
         rows[name] = _row(us, nbytes)
         del x, out

@@ -212,4 +212,9 @@ bool stream_plan(const eagle4_attn_args& a, StreamPlan& p);
 int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args& a);
 int stream_launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s);
 
+// ---- fp32 rows over fp32 pages (verify_attention_f32.hip) ----------------------------------------------------------
+bool f32_covered(const eagle4_attn_args& a);
+int64_t f32_workspace_bytes(const eagle4_attn_args& a);
+int f32_launch(const eagle4_attn_args& a, hipStream_t s);
+
 }  // namespace e4attn

@@ -368,10 +368,16 @@ Plan plan(const eagle4_attn_args& a) {
   return p;
 }
 
-bool covered(const eagle4_attn_args& a) {
+// The contract every schedule shares: GQA heads, at most 64 rows per request, int32 page table rows, head dim.
+bool shapes_ok(const eagle4_attn_args& a) {
   if (a.Hkv <= 0 || a.Hq % a.Hkv != 0 || a.max_query_len < 1 || a.max_query_len > 64 || a.page < 1) return false;
   if (a.block_table.dtype != EAGLE4_I32 || a.block_table.s1 != 1) return false;
-  if (a.D != 32 && a.D != 64 && a.D != 128 && a.D != 256) return false;
+  if (static_cast<int64_t>(a.max_blocks) * a.page >= (int64_t(1) << 31)) return false;  // 32-bit positions
+  return a.D == 32 || a.D == 64 || a.D == 128 || a.D == 256;
+}
+
+bool covered(const eagle4_attn_args& a) {
+  if (!shapes_ok(a)) return false;
   if (a.dtype != EAGLE4_BF16 && a.dtype != EAGLE4_F16) return false;
   if (a.cache_dtype != a.dtype && a.cache_dtype != EAGLE4_FP8_E4M3) return false;
   if (a.cache_dtype == EAGLE4_FP8_E4M3 && (a.k_scale == nullptr || a.v_scale == nullptr)) return false;
@@ -423,6 +429,7 @@ int launch_d(const eagle4_attn_args& a, const Plan& p, hipStream_t s) {
 }  // namespace
 
 extern "C" int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* a) {
+  if (a->dtype == EAGLE4_F32) return shapes_ok(*a) && f32_covered(*a) ? f32_workspace_bytes(*a) : -1;
   if (!covered(*a)) return -1;
   StreamPlan sp;
   if (stream_covered(*a) && stream_plan(*a, sp)) return stream_workspace_bytes(sp, *a);
@@ -432,11 +439,13 @@ extern "C" int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* a) 
   return parts * (a->D + 1) * static_cast<int64_t>(sizeof(float));
 }
 
-// 16-bit caches of up to 1024 requests take the streamed schedule; fp8 caches and larger batches the split one.
+// 16-bit rows: up to 1024 requests with the library's split take the streamed schedule (16-bit or fp8 pages), the
+// rest the split-context one. fp32 rows over fp32 pages: their own split-context kernel.
 extern "C" int eagle4_verify_attention(const eagle4_attn_args* a, void* stream) {
   if (a->num_reqs == 0) return EAGLE4_OK;
-  if (!covered(*a)) return EAGLE4_NOT_COVERED;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a->dtype == EAGLE4_F32) return shapes_ok(*a) && f32_covered(*a) ? f32_launch(*a, s) : EAGLE4_NOT_COVERED;
+  if (!covered(*a)) return EAGLE4_NOT_COVERED;
   StreamPlan sp;
   if (stream_covered(*a) && stream_plan(*a, sp)) {
     if (a->workspace == nullptr || a->workspace_bytes < stream_workspace_bytes(sp, *a)) return EAGLE4_NOT_COVERED;

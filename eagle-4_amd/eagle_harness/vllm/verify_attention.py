@@ -111,7 +111,7 @@ def verify_attention(
         chunk=chunk,
     )
     if q.dtype != out.dtype or q.dtype != k_new.dtype or q.dtype != v_new.dtype:
-        raise _native.NotCovered("q, k_new, v_new and out must share a 16-bit dtype")
+        raise _native.NotCovered("q, k_new, v_new and out must share a dtype (bf16, fp16, or fp32 over fp32 pages)")
     lib = _native.library()
     need = lib.eagle4_verify_attention_workspace(args)
     if need < 0:

@@ -117,6 +117,34 @@ def test_fp8_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, pa
         assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))
 
 
+@pytest.mark.parametrize(
+    "contexts, parents, heads, kv_heads, d, page",
+    [
+        ([300], [[-1, 0, 0, 1, 1, 2, 3]], 6, 1, 64, 16),
+        ([5, 700, 0], [[-1, 0, 1], [-1, 0, 0, 1, 2, 2, 3, 4, 5], [-1, 0]], 4, 2, 32, 32),
+        ([129], [[-1] + [r - 1 for r in range(1, 24)]], 6, 1, 64, 16),
+        ([1500, 2], [[-1, 0, 0, 1], [-1, 0]], 8, 2, 128, 16),
+        ([1000], [[-1, 0, 1, 1, 3, 0]], 12, 2, 256, 48),
+    ],
+)
+def test_fp32_matches_dense_oracle(dev, contexts, parents, heads, kv_heads, d, page):
+    """fp32 rows over fp32 pages (the reference's own test dtype): single and multi-split requests, ragged trees;
+    tolerance 1e-4 (fp32 sums in another order)."""
+    announce(f"attention fp32 contexts={contexts} heads={heads}/{kv_heads} d={d} page={page}")
+    inp = _inputs(contexts, parents, heads, kv_heads, d, page, torch.float32, seed=len(contexts) * 100 + heads + 3)
+    tokens = sum(len(p) for p in parents)
+    got = _run(dev, inp, torch.float32)
+    torch.testing.assert_close(got[:tokens], _want(inp)[:tokens], atol=1e-4, rtol=1e-4)
+    assert torch.equal(got[tokens:], torch.full_like(got[tokens:], 7.0))
+
+
+def test_fp32_b1_l512_workload(dev):
+    """The oracle's CPU case as is: batch 1, 16 seeded nodes, prefix 512, 16 / 4 heads, D 128, fp32."""
+    announce("attention b1 l512 fp32")
+    inp = attention_inputs(ATTN_B1, seed=1, dtype=torch.float32)
+    torch.testing.assert_close(_run(dev, inp, torch.float32), _want(inp), atol=1e-4, rtol=1e-4)
+
+
 def test_b1_l512_workload(dev):
     """Batch 1, 16 seeded nodes, prefix 512, 16 / 4 heads, D 128 (the oracle's fp32 CPU case, run in bf16)."""
     announce("attention b1 l512")
