@@ -296,7 +296,7 @@ def _records_chunk(steps: int) -> dict:
                                   width=x["width"])
 
         us[batch] = _time_graph(call, steps)
-        del x, g
+        del x
     return {"workload": "GDN records chunk form per layer: H16/HV48 K=V=128, 16-node trees, bf16 pool, bf16 q/k/v",
             "us_per_call": us, "reference_published_us": RECORDS_PUBLISHED_US,
             "speedup_vs_reference": {b: RECORDS_PUBLISHED_US[b] / us[b] for b in us}}
