@@ -3,10 +3,10 @@
 //
 // The 16-bit schedules' structure at fp32 width, on v_mfma_f32_16x16x4f32:
 //  * one workgroup per (context split, KV head, group of four 16-row tiles, request); a row is (draft token, query
-//    head of the KV head's group), so every K / V tile read serves G W rows; splits are 256-key context chunks, the
-//    last one also takes the draft keys (masked by the rows' ancestor bits); a request with several splits leaves
-//    fp32 partials with their log2-sum-exp, merged by a second kernel (kernels/online_softmax.py:11-24 and
-//    vllm/verify_attention.py:115-139);
+//    head of the KV head's group), so every K / V tile read serves G W rows; splits are context chunks (256 keys,
+//    fewer for grids too small to fill the chip), the last one also takes the draft keys (masked by the rows'
+//    ancestor bits); a request with several splits leaves fp32 partials with their log2-sum-exp, merged by a second
+//    kernel (kernels/online_softmax.py:11-24 and vllm/verify_attention.py:115-139);
 //  * 16-key tiles staged in LDS — K row-major (pitch D + 4 floats), V transposed to [d][key] (pitch 20 floats), both
 //    conflict-free for the 16-byte operand reads — the next tile held in registers while the current one computes;
 //  * S^T = K Q^T: block kb of the MFMA contracts over d = g D / 4 + kb for lane group g, so a lane's K and Q operands
@@ -21,9 +21,8 @@ namespace e4attn {
 
 namespace {
 
-constexpr int kKeysF = 16;    // keys per tile
-constexpr int kChunkF = 256;  // context keys per split
-constexpr int kTilesF = 4;    // 16-row tiles (waves) per workgroup
+constexpr int kKeysF = 16;  // keys per tile
+constexpr int kTilesF = 4;  // 16-row tiles (waves) per workgroup
 
 E4_DEV f32x4_t mma4(float a, float b, f32x4_t c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
 
@@ -40,7 +39,7 @@ struct ReqF {
   int width, context, splits;
 };
 
-E4_DEV ReqF req_f(const eagle4_attn_args& a, int b) {
+E4_DEV ReqF req_f(const eagle4_attn_args& a, int b, int chunk) {
   ReqF r;
   r.start = e4::ld(a.query_start_loc, b);
   const int64_t w = e4::ld(a.query_start_loc, b + 1) - r.start;
@@ -49,13 +48,13 @@ E4_DEV ReqF req_f(const eagle4_attn_args& a, int b) {
   const int64_t capacity = static_cast<int64_t>(a.max_blocks) * a.page;
   c = c < 0 ? 0 : (c > capacity ? capacity : c);
   r.context = static_cast<int>(c);
-  r.splits = c > 0 ? static_cast<int>((c + kChunkF - 1) / kChunkF) : 1;
+  r.splits = c > 0 ? static_cast<int>((c + chunk - 1) / chunk) : 1;
   return r;
 }
 
 // One workgroup: kTilesF waves of 16 rows; split blockIdx.x of request blockIdx.z, KV head and row group blockIdx.y.
 template <int D>
-__global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_attn_args a, int row_tiles,
+__global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_attn_args a, int chunk, int row_tiles,
                                                                  int max_splits) {
   using TL = TileF<D>;
   __shared__ __attribute__((aligned(16))) float sK[kKeysF * TL::KP];
@@ -65,7 +64,7 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
   const int G = a.Hq / a.Hkv;
   const int kvh = blockIdx.y % a.Hkv, rgroup = blockIdx.y / a.Hkv;
   const int b = blockIdx.z;
-  const ReqF rq = req_f(a, b);
+  const ReqF rq = req_f(a, b, chunk);
   if (split >= rq.splits || rq.width <= 0) return;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, c = lane & 15;
@@ -93,8 +92,8 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
   }
   const int64_t row_mask = row_ok ? a.masks[b * a.stride_mask + t] : 0;
 
-  const int lo = split * kChunkF;
-  const int hi = lo + kChunkF < rq.context ? lo + kChunkF : rq.context;
+  const int lo = split * chunk;
+  const int hi = lo + chunk < rq.context ? lo + chunk : rq.context;
   const bool has_new = split == rq.splits - 1;
   const int n_ctx = hi > lo ? (hi - lo + kKeysF - 1) / kKeysF : 0;
   const int n_tiles = n_ctx + (has_new ? (rq.width + kKeysF - 1) / kKeysF : 0);
@@ -230,11 +229,12 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
 // The splits of a row merged (vllm/verify_attention.py:115-139): weights 2^(lse_s - max) over the normalised
 // partials; one thread per 4 consecutive d of a row.
 template <int D>
-__global__ __launch_bounds__(256) void verify_f32_merge(const eagle4_attn_args a, int row_tiles, int max_splits) {
+__global__ __launch_bounds__(256) void verify_f32_merge(const eagle4_attn_args a, int chunk, int row_tiles,
+                                                        int max_splits) {
   constexpr int TPR = D / 4;
   constexpr int RPB = 256 / TPR;
   const int b = blockIdx.z, kvh = blockIdx.y;
-  const ReqF rq = req_f(a, b);
+  const ReqF rq = req_f(a, b, chunk);
   if (rq.splits <= 1 || rq.width <= 0) return;
   const int rho = blockIdx.x * RPB + threadIdx.x / TPR, d = 4 * (threadIdx.x % TPR);
   const int G = a.Hq / a.Hkv;
@@ -267,36 +267,40 @@ __global__ __launch_bounds__(256) void verify_f32_merge(const eagle4_attn_args a
 }
 
 struct PlanF {
-  int row_tiles, row_groups, max_splits;
+  int chunk, row_tiles, row_groups, max_splits;
 };
 
+// Context keys per split: a caller's choice, else 256, shortened (to 128, 64) while the grid of (request, KV head, row
+// group) workgroups is too small to occupy the chip.
 PlanF plan_f(const eagle4_attn_args& a) {
   PlanF p;
   p.row_tiles = e4::ceil_div(static_cast<int64_t>(a.Hq / a.Hkv) * a.max_query_len, 16);
   p.row_groups = e4::ceil_div(p.row_tiles, kTilesF);
+  const int64_t groups = static_cast<int64_t>(a.num_reqs) * a.Hkv * p.row_groups;
+  p.chunk = a.chunk > 0 ? a.chunk : (groups < 64 ? 64 : (groups < 256 ? 128 : 256));
   const int64_t capacity = static_cast<int64_t>(a.max_blocks) * a.page;
-  p.max_splits = capacity > 0 ? e4::ceil_div(capacity, kChunkF) : 1;
+  p.max_splits = capacity > 0 ? e4::ceil_div(capacity, p.chunk) : 1;
   return p;
 }
 
 template <int D>
 int launch_f(const eagle4_attn_args& a, const PlanF& p, hipStream_t s) {
   const dim3 grid(p.max_splits, a.Hkv * p.row_groups, a.num_reqs);
-  verify_f32_kernel<D><<<grid, 64 * kTilesF, 0, s>>>(a, p.row_tiles, p.max_splits);
+  verify_f32_kernel<D><<<grid, 64 * kTilesF, 0, s>>>(a, p.chunk, p.row_tiles, p.max_splits);
   if (p.max_splits > 1) {
     constexpr int RPB = 256 / (D / 4);
     const dim3 mgrid(e4::ceil_div(p.row_tiles * 16, RPB), a.Hkv, a.num_reqs);
-    verify_f32_merge<D><<<mgrid, 256, 0, s>>>(a, p.row_tiles, p.max_splits);
+    verify_f32_merge<D><<<mgrid, 256, 0, s>>>(a, p.chunk, p.row_tiles, p.max_splits);
   }
   return E4_LAUNCH_STATUS();
 }
 
 }  // namespace
 
-// fp32 rows over fp32 pages; 16-byte accesses along D (strides multiples of 4 elements); the rest of the contract is
-// checked by the caller.
+// fp32 rows over fp32 pages; 16-byte accesses along D (strides multiples of 4 elements); a caller's split a multiple
+// of the 16-key tile; the rest of the contract is checked by the caller.
 bool f32_covered(const eagle4_attn_args& a) {
-  return a.dtype == EAGLE4_F32 && a.cache_dtype == EAGLE4_F32 &&
+  return a.dtype == EAGLE4_F32 && a.cache_dtype == EAGLE4_F32 && a.chunk >= 0 && a.chunk % kKeysF == 0 &&
          ((a.stride_qt | a.stride_qh | a.stride_knt | a.stride_knh | a.stride_vnt | a.stride_vnh | a.stride_ot |
            a.stride_oh | a.stride_kb | a.stride_ks | a.stride_kh | a.stride_vb | a.stride_vs | a.stride_vh) %
           4) == 0;
