@@ -122,14 +122,15 @@ def gdn_tree_records_commit(
     assert records.shape[0] == L_layers and records.shape[3] == HV and state.stride(-1) == 1
     assert state.stride(3) == K and state.stride(2) == V * K, "contiguous (V, K) state per head"
     _records_layout(records, HV, V, K)
-    if records.shape[2] < parent.shape[1]:
-        raise _native.NotCovered("records must hold a step for every node of the parent table")
+    # the root path walks nodes below both the parent table's width and the records' steps (a parent table may be
+    # wider than the tree: its extra columns are never reached)
+    dmax = min(parent.shape[1], records.shape[2])
     args = _native.RecordsCommitArgs(
         state=state.data_ptr(), stride_state_layer=state.stride(0), stride_state_slot=state.stride(1),
         state_dtype=_native.dtype_code(state.dtype), round_state=int(bool(round_state)), records=records.data_ptr(),
         stride_records_layer=records.stride(0), stride_records_row=records.stride(1),
         state_indices=_native.itab(state_indices), record_indices=_native.itab(record_indices),
         commit_steps=_native.itab(commit_steps), parent=_native.itab(parent), n=n, layers=L_layers, HV=HV, K=K, V=V,
-        rec=records.shape[-1], dmax=parent.shape[1], reserved=0,
+        rec=records.shape[-1], dmax=dmax, reserved=0,
     )
     _native.launch("eagle4_gdn_tree_records_commit", args, state.device)

@@ -205,7 +205,8 @@ typedef struct eagle4_records_commit_args {
   eagle4_itab record_indices; /* [n] */
   eagle4_itab commit_steps;   /* [n] */
   eagle4_itab parent;         /* [n, width] */
-  int32_t n, layers, HV, K, V, rec, dmax;
+  int32_t n, layers, HV, K, V, rec;
+  int32_t dmax; /* root paths walk nodes below dmax: the parent table's width or the records' steps, the smaller */
   int32_t reserved;
 } eagle4_records_commit_args;
 int eagle4_gdn_tree_records_commit(const eagle4_records_commit_args* args, void* stream);

@@ -282,3 +282,149 @@ def test_chunk_then_commit_lands_on_the_walks_accepted_state(dev):
                                   num_accepted_tokens=torch.tensor([1], dtype=torch.int32), pad_slot_id=0)
     want = snaps[int(slots[0, accepted])]
     torch.testing.assert_close(pool[0, int(inp["state_indices"][0])].cpu(), want, atol=1e-5, rtol=1e-4)
+
+
+def _per_node_rounded(q, k, v, a, b, A, bias, state, slots, parent, width, batch, hv, h, rounded):
+    """Every node's state from its parent's, the parent rounded to the pool dtype first when ``rounded`` (the
+    reference test's independent form, tests/test_gdn_rounded_records_gpu.py:46-65): (outputs like v, per-request
+    node states)."""
+    K = k.shape[-1]
+    expected = torch.empty_like(v)
+    snapshots = []
+    for request in range(batch):
+        states = []
+        for node in range(width):
+            token = request * width + node
+            prior = state[int(slots[request])].float() if node == 0 else states[int(parent[request, node])]
+            if rounded and node > 0:
+                prior = prior.to(state.dtype).float()
+            key = k[0, token].float()
+            key = key / (key.square().sum(-1, keepdim=True) + 1e-6).sqrt()
+            query = q[0, token].float()
+            query = query / (query.square().sum(-1, keepdim=True) + 1e-6).sqrt() / K**0.5
+            key, query = key.repeat_interleave(hv // h, 0), query.repeat_interleave(hv // h, 0)
+            decay = (-A.exp() * torch.nn.functional.softplus(a[token].float() + bias)).exp()
+            beta = b[token].float().sigmoid().to(b.dtype).float()
+            decayed = prior * decay[:, None, None]
+            delta = (v[0, token].float() - (decayed * key[:, None, :]).sum(-1)) * beta[:, None]
+            current = decayed + delta[:, :, None] * key[:, None, :]
+            states.append(current)
+            expected[0, token] = (current * query[:, None, :]).sum(-1).to(v.dtype)
+        snapshots.append(states)
+    return expected, snapshots
+
+
+@pytest.mark.parametrize("width,batch", [(1, 1), (8, 2), (16, 1), (32, 2)])
+@pytest.mark.parametrize("state_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rounded", [True, False], ids=["path_replay", "chunk"])
+def test_reference_rounded_records_scenario(dev, width, batch, state_dtype, rounded):
+    """The reference's own GPU scenario (tests/test_gdn_rounded_records_gpu.py:10-113): one path row per node (each
+    writing only its node), slots and record rows in reverse, a parent table wider than the tree, spare record steps
+    and rows left alone; outputs against the per-node form (rounded parents for the path replay, none for the chunk)
+    and the oracle; the commit of the last node against its state; a negative step and an int64 parent table."""
+    from eagle_harness.kernels.gdn_tree_records import (gdn_tree_chunk_update, gdn_tree_records_commit,
+                                                        gdn_tree_records_update)
+
+    announce(f"records reference scenario width={width} batch={batch} {state_dtype} rounded={rounded}")
+    gen = torch.Generator().manual_seed(41 + width)
+    h, hv, K, V = 4, 12, 128, 128
+
+    def rand(*shape, dtype=torch.bfloat16):
+        return (torch.randn(*shape, generator=gen) * 0.2).to(dtype)
+
+    q, k = rand(1, batch * width, h, K), rand(1, batch * width, h, K)
+    v = rand(1, batch * width, hv, V)
+    a, b = rand(batch * width, hv), rand(batch * width, hv)
+    A, bias = rand(hv, dtype=torch.float32), rand(hv, dtype=torch.float32)
+    state = rand(batch + 2, hv, V, K, dtype=state_dtype)
+    slots = torch.arange(1, batch + 1, dtype=torch.int32).flip(0)
+    rows = torch.arange(batch, dtype=torch.int32).flip(0)
+    qsl = torch.arange(batch + 1, dtype=torch.int32) * width
+    parent = torch.zeros(batch, width + 7, dtype=torch.int32)
+    for node in range(1, width):
+        parent[:, node] = torch.randint(node, (batch,), generator=gen, dtype=torch.int32)
+    paths = torch.zeros(batch, width, width + 2, dtype=torch.int32)
+    for request in range(batch):
+        for node in range(width):
+            chain = [node]
+            while chain[-1] > 0:
+                chain.append(int(parent[request, chain[-1]]))
+            chain.reverse()
+            paths[request, node, 0], paths[request, node, 1] = len(chain), len(chain) - 1
+            paths[request, node, 2 : 2 + len(chain)] = torch.tensor(chain, dtype=torch.int32)
+    rec = torch.full((batch + 1, width + 3, hv, V + K + 4), SENTINEL)
+    expected, snapshots = _per_node_rounded(q, k, v, a, b, A, bias, state, slots, parent, width, batch, hv, h, rounded)
+    want_rec = rec.clone()
+    if rounded:
+        want = orec.gdn_tree_records_update(A, bias, q, k, v, a, b, state=state, state_indices=slots,
+                                            query_start_loc=qsl, parent=parent, tree_paths=paths, records=want_rec,
+                                            record_indices=rows, width=width)
+    else:
+        want = orec.gdn_tree_chunk_update(A, bias, q, k, v, a, b, state=state, state_indices=slots,
+                                          query_start_loc=qsl, parent=parent, records=want_rec, record_indices=rows,
+                                          width=width)
+    # the oracle against the per-node form first (outputs are 16-bit: a rounding step apart at most)
+    torch.testing.assert_close(want.float(), expected.float(), atol=2e-3, rtol=2e-2)
+    g = _to(dict(q=q, k=k, v=v, a=a, b=b, A=A, bias=bias, state=state, slots=slots, rows=rows, qsl=qsl,
+                 parent=parent, paths=paths, rec=rec), dev)
+    kw = dict(state=g["state"], state_indices=g["slots"], query_start_loc=g["qsl"], parent=g["parent"],
+              records=g["rec"], record_indices=g["rows"], width=width)
+    if rounded:
+        out = gdn_tree_records_update(g["A"], g["bias"], g["q"], g["k"], g["v"], g["a"], g["b"], tree_paths=g["paths"],
+                                      **kw)
+    else:
+        out = gdn_tree_chunk_update(g["A"], g["bias"], g["q"], g["k"], g["v"], g["a"], g["b"], **kw)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), expected.float(), atol=2e-3, rtol=2e-2)
+    _compare(out, want, g["rec"], want_rec, False, K, V)
+    assert bool((g["rec"][-1] == SENTINEL).all().item())  # the unused record row
+    accepted = torch.full((batch,), width - 1, dtype=torch.int32, device=dev)
+    committed = g["state"].clone().unsqueeze(0)
+    gdn_tree_records_commit(committed, g["rec"].unsqueeze(0), g["slots"], g["rows"], accepted, g["parent"], rounded)
+    torch.cuda.synchronize()
+    for request in range(batch):
+        torch.testing.assert_close(committed[0, int(slots[request])].cpu().float(),
+                                   snapshots[request][-1].to(state_dtype).float(), atol=2e-3, rtol=2e-2)
+    assert torch.equal(committed[0, 0].cpu(), state[0]) and torch.equal(committed[0, -1].cpu(), state[-1])
+    before = committed.clone()
+    gdn_tree_records_commit(committed, g["rec"].unsqueeze(0), g["slots"], g["rows"], -torch.ones_like(accepted),
+                            g["parent"], rounded)
+    torch.cuda.synchronize()
+    assert torch.equal(committed, before)  # a negative step touches nothing
+    from_int64 = g["state"].clone().unsqueeze(0)
+    gdn_tree_records_commit(from_int64, g["rec"].unsqueeze(0), g["slots"], g["rows"], accepted,
+                            g["parent"].to(torch.int64), rounded)
+    torch.cuda.synchronize()
+    assert torch.equal(from_int64, committed)
+
+
+def test_parent_rounding_does_not_accumulate_sub_ulp_decay_on_the_device(dev):
+    """The reference's known answer (tests/test_gdn_rounded_records_gpu.py:116-162): a 32-node chain from an all-ones
+    bf16 state whose per-node decay is below half a bf16 ulp — every rounded parent is the pool state again, so every
+    output is the first one and the rounded commit leaves the pool bit for bit."""
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_commit, gdn_tree_records_update
+
+    announce("records sub-ulp decay chain")
+    width, dim = 32, 128
+    state = torch.ones(1, 1, dim, dim, device=dev, dtype=torch.bfloat16)
+    q = torch.zeros(1, width, 1, dim, device=dev, dtype=torch.bfloat16)
+    q[..., 0] = 1
+    k, v = torch.zeros_like(q), torch.zeros_like(q)
+    a = torch.full((width, 1), -7.0, device=dev, dtype=torch.bfloat16)
+    b = torch.zeros_like(a)
+    A = torch.zeros(1, device=dev)
+    slot = torch.zeros(1, device=dev, dtype=torch.int32)
+    qsl = torch.tensor([0, width], device=dev, dtype=torch.int32)
+    parent = (torch.arange(width, device=dev, dtype=torch.int32) - 1).view(1, width)
+    paths = torch.cat((torch.tensor([width, 0], device=dev, dtype=torch.int32),
+                       torch.arange(width, device=dev, dtype=torch.int32))).view(1, 1, width + 2)
+    records = torch.empty(1, width, 1, dim * 2 + 4, device=dev)
+    out = gdn_tree_records_update(A, A, q, k, v, a, b, state=state, state_indices=slot, query_start_loc=qsl,
+                                  parent=parent, tree_paths=paths, records=records, record_indices=slot, width=width)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out[:, :1].expand_as(out))
+    committed = state.clone().unsqueeze(0)
+    gdn_tree_records_commit(committed, records.unsqueeze(0), slot, slot, torch.full_like(slot, width - 1), parent,
+                            True)
+    torch.cuda.synchronize()
+    assert torch.equal(committed[0], state)
