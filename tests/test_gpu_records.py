@@ -428,3 +428,33 @@ def test_parent_rounding_does_not_accumulate_sub_ulp_decay_on_the_device(dev):
                             True)
     torch.cuda.synchronize()
     assert torch.equal(committed[0], state)
+
+
+def test_commit_layer_offsets_past_2_31_elements(dev):
+    """The reference's known answer for 64-bit layer offsets (tests/test_gdn_tree_records_gpu.py:94-122): a pool
+    whose later layers start past 2^31 elements, behind a guard region one layer long; the commit lands only in its
+    slot of every layer."""
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_commit
+
+    announce("records commit past 2^31 elements")
+    heads, dim, slots = 8, 128, 8193
+    layer = slots * heads * dim * dim
+    assert layer < 2**31 <= 2 * layer
+    pool = torch.zeros(4 * layer, dtype=torch.bfloat16, device=dev)
+    guard, state = pool[:layer], pool[layer:].view(3, slots, heads, dim, dim)
+    slot = slots - 1
+    gen = torch.Generator(device=dev).manual_seed(5)
+    before = torch.randn(3, heads, dim, dim, generator=gen, device=dev).to(torch.bfloat16)
+    state[:, slot] = before
+    records = torch.randn(3, 1, 1, heads, 2 * dim + 4, generator=gen, device=dev)
+    records[..., 2 * dim] = torch.rand(3, 1, 1, heads, generator=gen, device=dev)
+    one = torch.ones(1, dtype=torch.int32, device=dev)
+    root = torch.zeros(1, 1, dtype=torch.int32, device=dev)
+    gdn_tree_records_commit(state, records, one * slot, one * 0, one * 0, root, False)
+    torch.cuda.synchronize()
+    delta, key, decay = records[:, 0, 0, :, :dim], records[:, 0, 0, :, dim : 2 * dim], records[:, 0, 0, :, 2 * dim]
+    want = before.float() * decay[..., None, None] + delta[..., :, None] * key[..., None, :]
+    torch.testing.assert_close(state[:, slot].float(), want.to(torch.bfloat16).float(), atol=0.01, rtol=0.01)
+    assert not guard.any().item(), "a layer's commit landed outside the pool"
+    assert not state[:, :slot].any().item(), "a commit landed in another slot"
+    del pool

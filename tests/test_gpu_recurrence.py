@@ -234,3 +234,43 @@ def test_full_batch_sampled_requests_match_oracle(dev):
         torch.testing.assert_close(o_got[:, sl].cpu().float(), want.float(), atol=2e-2, rtol=1e-2)
         idx = sub_slots[0].long()
         _state_close(g["pool"][idx.to(dev)].cpu(), pool[idx])
+
+
+def test_packed_projection_views_equal_contiguous_inputs(dev):
+    """The callers' layout (tests/test_gdn_tree_kernels.py:222-309; vllm/gdn_tree_verify.py:84-100): q / k / v as
+    token-strided views of one packed projection [tokens, 2 H K + HV V (+ z)] and b / a as the halves of [tokens, 2 HV]
+    give the same outputs and snapshots, bit for bit, as contiguous copies of the same values."""
+    from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+
+    announce("recurrence packed projection views")
+    gen = torch.Generator().manual_seed(23)
+    plists = [_random_tree(8, 4), TREE]
+    width = max(map(len, plists))
+    heads, value_heads, dk, dv = 2, 4, 128, 128
+    key_dim, value_dim = heads * dk, value_heads * dv
+    dim = 2 * key_dim + value_dim
+    parents, qsl = _requests(plists, width)
+    tokens = int(qsl[-1])
+    qkvz = torch.randn(tokens, dim + value_dim, generator=gen).bfloat16().to(dev)  # [q, k, v, z]
+    ba = torch.randn(tokens, 2 * value_heads, generator=gen).bfloat16().to(dev)
+    b, a = ba.chunk(2, dim=-1)
+    A_log, dt_bias = torch.randn(value_heads, generator=gen).to(dev), torch.randn(value_heads, generator=gen).to(dev)
+    slots = torch.arange(1, 1 + len(plists) * (width + 1), dtype=torch.int32).view(len(plists), width + 1).to(dev)
+    state0 = (torch.randn(slots.numel() + 2, value_heads, dv, dk, generator=gen) * 0.1).to(dev)
+    accepted = torch.tensor([1, 2], dtype=torch.int32, device=dev)
+    parents, qsl = parents.to(dev), qsl.to(dev)
+    q, k, v = qkvz[:, :key_dim], qkvz[:, key_dim : 2 * key_dim], qkvz[:, 2 * key_dim : dim]
+
+    def run(q, k, v, a, b):
+        state = state0.clone()
+        out = gdn_tree_recurrent_update(A_log, dt_bias, q.view(1, tokens, heads, dk), k.view(1, tokens, heads, dk),
+                                        v.view(1, tokens, value_heads, dv), a, b, initial_state_source=state,
+                                        initial_state_indices=slots, cu_seqlens=qsl, intermediate_states_buffer=state,
+                                        intermediate_state_indices=slots, retrieve_parent_token=parents,
+                                        num_accepted_tokens=accepted, pad_slot_id=0)
+        torch.cuda.synchronize()
+        return out, state
+
+    o_views, s_views = run(q, k, v, a, b)
+    o_flat, s_flat = run(q.contiguous(), k.contiguous(), v.contiguous(), a.contiguous(), b.contiguous())
+    assert torch.equal(o_views, o_flat) and torch.equal(s_views, s_flat)

@@ -133,9 +133,3 @@ def test_tail_words_match_oracle(dev, width, kv_len):
     assert tail[:width].cpu().tolist() == want == closed
     assert int(tail[width]) == 7
 
-
-def test_tail_width_over_a_word_is_rejected():
-    from eagle_harness.kernels.verify_prep import tree_tail_words
-
-    with pytest.raises(ValueError, match="verify width 65"):
-        tree_tail_words(None, None, None, width=65)
