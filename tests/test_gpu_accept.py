@@ -133,3 +133,73 @@ def test_linear_state_commit_matches_oracle(dev, ssm_dtype):
     for layer in range(layers):
         assert torch.equal(gc[layer].cpu(), want_c[layer])
         assert torch.equal(gs[layer].cpu(), want_s[layer])
+
+
+def _linked_tree(width, rng):
+    """A random tree as first-child / next-sibling links (about half the nodes continue a chain), draft tokens in a
+    small vocabulary and a target that follows a child's draft 80 % of the time (the shape of
+    tests/test_accept_tail_gpu.py:23-39)."""
+    parent = [-1] + [rng.randrange(0, i) if rng.random() < 0.5 else i - 1 for i in range(1, width)]
+    kids = [[j for j in range(width) if parent[j] == i] for i in range(width)]
+    first = [c[0] if c else -1 for c in kids]
+    sibling = [-1] * width
+    for c in kids:
+        for x, y in zip(c, c[1:]):
+            sibling[x] = y
+    cand = [rng.randrange(0, 6) for _ in range(width)]
+    target = [cand[rng.choice(kids[i])] if kids[i] and rng.random() < 0.8 else rng.randrange(0, 6) for i in range(width)]
+    return cand, first, sibling, target
+
+
+@pytest.mark.parametrize("width,depth", [(16, 12), (9, 8), (4, 4), (2, 2), (31, 12), (32, 32), (8, 1)])
+def test_accept_tail_served_shapes(dev, width, depth):
+    """The widths and depths the reference serves after its warm-up (tests/test_accept_tail_gpu.py:69-153):
+    int64 tables, an out_cache_loc that is a slice of a slot list (8-byte aligned), compaction into the rows of a
+    wider hidden buffer; every field against the oracle."""
+    import random
+
+    from eagle_harness.kernels.accept_tail import accept_tail, compact_rows, warm_up
+
+    announce(f"accept tail width={width} depth={depth}")
+    hidden = torch.zeros(64, 5120, dtype=torch.bfloat16, device=dev)
+    warm_up(hidden, torch.bfloat16)
+    rng = random.Random(7 + width * 100 + depth)
+    cand, first, sibling, target = _linked_tree(width, rng)
+    long = dict(dtype=torch.int64)
+    slots_all = torch.tensor([rng.randrange(1, 1 << 20) for _ in range(width + 1)], **long)
+    args = (torch.tensor(target, **long), torch.tensor(cand, **long), torch.arange(width, **long).reshape(1, width),
+            torch.tensor(first, **long).reshape(1, width), torch.tensor(sibling, **long).reshape(1, width),
+            torch.tensor([rng.randrange(1, 150)], **long), slots_all[1:],
+            torch.tensor([[rng.randrange(1, 1 << 20) for _ in range(200 + width)] for _ in range(3)], dtype=torch.int32),
+            torch.tensor([1], **long))
+    want = oacc.accept_tail(*args, depth)
+    slots_dev = slots_all.to(dev)
+    dev_args = [x.to(dev) for x in args]
+    dev_args[6] = slots_dev[1:]  # the slice itself, not a copy: its data starts 8 bytes into the allocation
+    got = accept_tail(*dev_args, depth)
+    rows = torch.randn(width, 5120, generator=torch.Generator().manual_seed(width)).to(torch.bfloat16)
+    compact_rows(rows.to(dev), got.accept_index, out=hidden[:width])
+    torch.cuda.synchronize()
+    for name in want:
+        assert getattr(got, name).cpu().tolist() == want[name].tolist(), name
+    assert torch.equal(hidden[:width].cpu(), oacc.compact_rows(rows, want["accept_index"]))
+    assert not hidden[width:].any().item()
+
+
+def test_graph_capture_stages_the_tree_path_whatever_was_staged_last(dev):
+    """The layers ask ``VerifyStage.verifying``; it is true while a graph is captured even when the last staged batch
+    was a chain (tests/test_gpu_kernels.py:113-125)."""
+    from eagle_harness.vllm.verify_layout import VerifyStage
+
+    announce("verify stage graph capture")
+    stage = VerifyStage(2, 16, 8, dev)
+    stage.active = False
+    assert not stage.verifying
+    seen = []
+    torch.zeros(1, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        seen.append(stage.verifying)
+    assert seen == [True]
+    stage.active = True
+    assert stage.verifying
