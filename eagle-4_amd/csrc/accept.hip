@@ -26,16 +26,40 @@ __global__ __launch_bounds__(256) void argmax_kernel(const eagle4_argmax_args a)
   int64_t bi = INT64_MAX;
   const bool aligned = (reinterpret_cast<uintptr_t>(p) % 16) == 0;
   const int nvec = aligned ? a.vocab / VEC : 0;
-  for (int v = threadIdx.x; v < nvec; v += blockDim.x) {
-    const uint4 raw = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(v) * VEC);
-    const S* e = reinterpret_cast<const S*>(&raw);
+  // UNR 16-byte loads in flight per thread before any is reduced (a thread's vectors are v, v + 256, ...; positions
+  // past the row re-read its first vector and are skipped)
+  constexpr int UNR = 4;
+  for (int v0 = threadIdx.x; v0 < nvec; v0 += UNR * blockDim.x) {
+    uint4 raw[UNR];
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) {
-      const float f = T::to_f32(e[i]);
-      const int64_t idx = static_cast<int64_t>(v) * VEC + i;
-      if (better(f, idx, bv, bi)) {
-        bv = f;
-        bi = idx;
+    for (int u = 0; u < UNR; ++u) {
+      const int v = v0 + u * static_cast<int>(blockDim.x);
+      raw[u] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(v < nvec ? v : 0) * VEC);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int v = v0 + u * static_cast<int>(blockDim.x);
+      const S* e = reinterpret_cast<const S*>(&raw[u]);
+      float f[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) f[i] = T::to_f32(e[i]);
+      // the vector's max (NaN-ignoring) and sum (NaN when a NaN, or opposite infinities, is in it): only a vector
+      // that can change the thread's best — a larger value, a NaN, or the thread's first vector — is searched
+      float m = f[0], sum = f[0];
+#pragma unroll
+      for (int i = 1; i < VEC; ++i) {
+        m = fmaxf(m, f[i]);
+        sum += f[i];
+      }
+      if (v < nvec && (m > bv || sum != sum || bi == INT64_MAX)) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+          const int64_t idx = static_cast<int64_t>(v) * VEC + i;
+          if (better(f[i], idx, bv, bi)) {
+            bv = f[i];
+            bi = idx;
+          }
+        }
       }
     }
   }
