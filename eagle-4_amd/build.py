@@ -35,11 +35,12 @@ HIPCC_FLAGS = [
 ]
 
 
-# Per-file additions. The streamed attention and tree-chunk kernels keep their MFMA accumulators in VGPRs (the default
+# Per-file additions. The streamed attention, tree-chunk and tree-replay kernels keep their MFMA accumulators in VGPRs (the default
 # AGPR form makes LLVM shuttle them between the two register files: every iteration in the attention kernel, for every
-# accumulator the chunk kernel's VALU math reads).
+# accumulator the chunk and replay kernels' VALU math reads).
 EXTRA_FLAGS = {"verify_attention_stream.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-               "gdn_tree_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+               "gdn_tree_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+               "gdn_tree_replay.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def _hipcc() -> str:

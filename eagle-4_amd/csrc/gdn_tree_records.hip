@@ -23,6 +23,10 @@ namespace e4chunk {
 // gdn_tree_chunk.hip: the chunk form on the matrix cores (trees of <= 16 nodes, bf16 inputs)
 int launch(const eagle4_records_args& a, hipStream_t s) __attribute__((visibility("hidden")));
 }
+namespace e4replay {
+// gdn_tree_replay.hip: the rounded path replay on the matrix cores (16-bit inputs and pool of one dtype)
+int launch(const eagle4_records_args& a, hipStream_t s) __attribute__((visibility("hidden")));
+}
 
 namespace {
 
@@ -490,8 +494,8 @@ extern "C" int eagle4_gdn_tree_records_update(const eagle4_records_args* a, void
       reinterpret_cast<uintptr_t>(a->q) % (4 * esz) || reinterpret_cast<uintptr_t>(a->k) % (4 * esz) ||
       reinterpret_cast<uintptr_t>(a->v) % (4 * esz))
     return EAGLE4_NOT_COVERED;
-  if (!a->path_replay) {
-    const int st = e4chunk::launch(*a, s);
+  {
+    const int st = a->path_replay ? e4replay::launch(*a, s) : e4chunk::launch(*a, s);
     if (st != EAGLE4_NOT_COVERED) return st;
   }
   switch (a->K) {

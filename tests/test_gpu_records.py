@@ -118,6 +118,70 @@ def test_request_without_records_runs_as_one_chain(dev):
     _compare(got, want, g["records"], want_rec, False, 64, 32)
 
 
+def _nested_branches(levels):
+    """A chain c_0 .. c_levels whose every node but the last also has a side child s_i with one leaf, the last two
+    leaves: `levels` nested nodes whose two children both have children, parent first."""
+    par = [-1]
+    chain = [0]
+    for _ in range(levels):
+        chain.append(len(par))
+        par.append(chain[-2])
+    side = []
+    for i in range(levels):
+        side.append(len(par))
+        par.append(chain[i])
+    for s in side:
+        par.append(s)
+    par += [chain[-1], chain[-1]]
+    return par
+
+
+def _replay_case(dev, trees, dims, in_dtype, pool_dtype, seed):
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
+
+    inp, width = _inputs(trees, *dims, pool_dtype, in_dtype=in_dtype, seed=seed)
+    want_rec = inp["records"].clone()
+    want = orec.gdn_tree_records_update(inp["A_log"], inp["dt_bias"], inp["q"], inp["k"], inp["v"], inp["a"],
+                                        inp["b"], state=inp["state"], state_indices=inp["state_indices"],
+                                        query_start_loc=inp["query_start_loc"], parent=inp["parent"],
+                                        tree_paths=inp["tree_paths"], records=want_rec,
+                                        record_indices=inp["record_indices"], width=width)
+    g = _to(inp, dev)
+    got = _call(gdn_tree_records_update, g, width, tree_paths=g["tree_paths"])
+    torch.cuda.synchronize()
+    _compare(got, want, g["records"], want_rec, False, dims[2], dims[3])
+    assert torch.equal(g["state"].cpu(), inp["state"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dims", [(4, 8, 128, 128), (2, 4, 64, 32), (1, 2, 256, 128), (2, 2, 32, 64)])
+def test_path_replay_same_dtype_head_dims(dev, dtype, dims):
+    """16-bit inputs and pool of one dtype take the matrix-core replay: trees of 1-16 nodes (a chain, a star, seeded
+    ones), every head dim it covers."""
+    announce(f"records path replay {dtype} dims={dims}")
+    rng = np.random.default_rng(60)
+    trees = [seeded_tree(rng, 16), [-1], [-1, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0], [-1, 0, 1, 2, 3, 4, 5], seeded_tree(rng, 9)]
+    _replay_case(dev, trees, dims, dtype, dtype, 61)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_path_replay_wide_trees(dev, dtype):
+    """Trees of 17-64 nodes: stars wider than one MFMA pass of eight children, deep seeded trees."""
+    announce(f"records path replay wide trees {dtype}")
+    rng = np.random.default_rng(62)
+    trees = [seeded_tree(rng, 64), [-1] + [0] * 30, seeded_tree(rng, 40), [-1, 0, 1] + [2] * 17]
+    _replay_case(dev, trees, (2, 4, 128, 128), dtype, dtype, 63)
+
+
+@pytest.mark.parametrize("levels,dims", [(4, (2, 4, 128, 128)), (6, (2, 4, 64, 64)), (3, (1, 2, 256, 128))])
+def test_path_replay_nested_branches_outgrow_the_parked_states(dev, levels, dims):
+    """More nested nodes with two branching children than the replay parks: the oldest parked states are dropped and
+    recomputed from the pool state along their root paths."""
+    announce(f"records path replay nested branches levels={levels} dims={dims}")
+    rng = np.random.default_rng(64)
+    _replay_case(dev, [_nested_branches(levels), seeded_tree(rng, 12)], dims, torch.bfloat16, torch.bfloat16, 65)
+
+
 @pytest.mark.parametrize("dims", [(4, 8, 128, 128), (2, 2, 64, 32), (1, 2, 256, 128)])
 def test_chunk_form_matches_oracle_closed_form(dev, dims):
     from eagle_harness.kernels.gdn_tree_records import gdn_tree_records_update
