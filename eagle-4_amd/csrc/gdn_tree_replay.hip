@@ -11,13 +11,14 @@
 // fp32 sums). Only a node with children needs its own state, h~_j = round(e_j h~_p + k^_j delta_j^T): a fused
 // multiply-add per element and the hardware's packed round-to-nearest-even conversion. Leaves cost no state work.
 //
-// One wave owns 16 V rows of one (request, value head); a workgroup of two waves shares the request's staged node
+// One wave owns 16 V rows of one (request, value head); a workgroup of four waves shares the request's staged node
 // inputs in LDS. The state lives in registers as the MFMA's 16-bit operand (lane: row r16, K elements
 // [g K / 4, (g + 1) K / 4) in blocks of 8). The wave walks the tree's internal nodes depth first: a node whose several
 // children have children of their own parks its rounded state in a small register stack (the oldest entry is dropped
 // when it is full); a parent whose entry was dropped is recomputed from the pool state along its root path with the
-// deltas already in LDS. A request without records (record_indices < 0) runs its rows as one chain with an fp32
-// state and no rounding (:51-53).
+// deltas already in LDS. Deltas and output terms gather in LDS and leave at the end as 16- and 8-byte row runs. A
+// request without records (record_indices < 0) runs its rows as one chain with an fp32 state and no rounding
+// (:51-53).
 
 #include "gdn_walk.h"
 
@@ -38,7 +39,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // 16 bytes as a native vector: arrays of it stay in registers (arrays of the uint4 struct can land in scratch memory)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int WAVES = 2;          // waves per workgroup
+constexpr int WAVES = 4;          // waves per workgroup
 constexpr int NT = 64 * WAVES;    // threads per workgroup
 constexpr int ROWS = 16 * WAVES;  // V rows per workgroup
 
@@ -58,6 +59,7 @@ struct Ops<e4::Bf16> {
     const f32x2_t v = {x0, x1};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
   }
+  static E4_DEV uint16_t narrow(float x) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x)); }
 };
 template <>
 struct Ops<e4::F16> {
@@ -71,6 +73,7 @@ struct Ops<e4::F16> {
     const f32x2_t v = {x0, x1};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
   }
+  static E4_DEV uint16_t narrow(float x) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x)); }
 };
 
 
@@ -78,82 +81,91 @@ struct Ops<e4::F16> {
 // just before; LDS executes one wave's accesses in order).
 E4_DEV void lds_order() { __asm__ volatile("" ::: "memory"); }
 
-// ---- a request without records: one chain over its rows, fp32 state, no rounding (:51-53, :77-92) ----------------------
-// Lane (g, r16): V row `row`, K elements [g K / 4, (g + 1) K / 4). A rare path, kept small in registers: the raw q / k
-// words are widened where they are used.
+// ---- a request without records: one chain over its rows, fp32 state, no rounding (:51-53, :77-92) ------------------
+// A rare path, kept small in registers so it does not cost the tree walk occupancy: the wave's 16 rows in two halves
+// of 8, lane (g8, r8) holding row r8 of the half and K elements [g8 K / 8, (g8 + 1) K / 8), the raw q / k words
+// widened where they are used.
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 template <int K, typename T>
-E4_DEV void chain_walk(const eagle4_records_args& a, int64_t bos, int Tn, int idx, int hv, int ih, int row, int g,
-                       float A, float dt_bias) {
+E4_DEV void chain_walk(const eagle4_records_args& a, int64_t bos, int Tn, int idx, int hv, int ih, int row16,
+                       int lane, float A, float dt_bias) {
   using O = Ops<T>;
-  constexpr int KQ = K / 4, CH = KQ / 8;
-  float h[KQ];
-  {
-    const uint16_t* sp = static_cast<const uint16_t*>(a.state) + (idx >= 0 ? idx : 0) * a.stride_state +
-                         (static_cast<int64_t>(hv) * a.V + row) * K + g * KQ;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const u32x4 raw = idx >= 0 ? *reinterpret_cast<const u32x4*>(sp + 8 * c) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        h[8 * c + 2 * e] = O::lo(raw[e]);
-        h[8 * c + 2 * e + 1] = O::hi(raw[e]);
-      }
-    }
-  }
+  constexpr int EL = K / 8, CH = EL / 4;  // elements per lane, in 8-byte chunks
+  const int r8 = lane & 7, g8 = lane >> 3;
   auto reduce = [](float x) {
+    x += __shfl_xor(x, 8);
     x += __shfl_xor(x, 16);
     return x + __shfl_xor(x, 32);
   };
-  for (int t = 0; t < Tn; ++t) {
-    const int64_t tok = bos + t;
-    const uint16_t* kp = static_cast<const uint16_t*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K + g * KQ;
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K + g * KQ;
-    u32x4 kr[CH], qr[CH];
+  for (int half = 0; half < 2; ++half) {
+    const int row = row16 + 8 * half + r8;
+    float h[EL];
+    {
+      const uint16_t* sp = static_cast<const uint16_t*>(a.state) + (idx >= 0 ? idx : 0) * a.stride_state +
+                           (static_cast<int64_t>(hv) * a.V + row) * K + g8 * EL;
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      kr[c] = *reinterpret_cast<const u32x4*>(kp + 8 * c);
-      qr[c] = *reinterpret_cast<const u32x4*>(qp + 8 * c);
+      for (int c = 0; c < CH; ++c) {
+        const u32x2 raw = idx >= 0 ? *reinterpret_cast<const u32x2*>(sp + 4 * c) : u32x2{0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          h[4 * c + 2 * e] = O::lo(raw[e]);
+          h[4 * c + 2 * e + 1] = O::hi(raw[e]);
+        }
+      }
     }
-    const uint16_t vraw = static_cast<const uint16_t*>(a.v)[tok * a.stride_v + static_cast<int64_t>(hv) * a.V + row];
-    const uint32_t ga = load_raw(a.a, tok * a.stride_a + hv, a.gate_dtype);
-    const uint32_t gb = load_raw(a.b, tok * a.stride_b + hv, a.gate_dtype);
-    float kk = 0.f, qq = 0.f;
+    for (int t = 0; t < Tn; ++t) {
+      const int64_t tok = bos + t;
+      const int64_t head = static_cast<int64_t>(ih) * K + g8 * EL;
+      const uint16_t* kp = static_cast<const uint16_t*>(a.k) + tok * a.stride_k + head;
+      const uint16_t* qp = static_cast<const uint16_t*>(a.q) + tok * a.stride_q + head;
+      u32x2 kr[CH], qr[CH];
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float k0 = O::lo(kr[c][e]), k1 = O::hi(kr[c][e]), q0 = O::lo(qr[c][e]), q1 = O::hi(qr[c][e]);
-        kk = fmaf(k0, k0, fmaf(k1, k1, kk));
-        qq = fmaf(q0, q0, fmaf(q1, q1, qq));
+      for (int c = 0; c < CH; ++c) {
+        kr[c] = *reinterpret_cast<const u32x2*>(kp + 4 * c);
+        qr[c] = *reinterpret_cast<const u32x2*>(qp + 4 * c);
       }
-    const float ks = 1.0f / sqrtf(reduce(kk) + 1e-6f), qs = a.scale / sqrtf(reduce(qq) + 1e-6f);  // (:147-150)
-    const float2 gt = gate_of(ga, gb, a.gate_dtype, 1.0f, 20.0f, A, dt_bias);
-    float hk = 0.f;
+      const uint16_t vraw = static_cast<const uint16_t*>(a.v)[tok * a.stride_v + static_cast<int64_t>(hv) * a.V + row];
+      const uint32_t ga = load_raw(a.a, tok * a.stride_a + hv, a.gate_dtype);
+      const uint32_t gb = load_raw(a.b, tok * a.stride_b + hv, a.gate_dtype);
+      float kk = 0.f, qq = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+      for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float& h0 = h[8 * c + 2 * e];
-        float& h1 = h[8 * c + 2 * e + 1];
-        h0 *= gt.x;
-        h1 *= gt.x;
-        hk = fmaf(h0, O::lo(kr[c][e]), fmaf(h1, O::hi(kr[c][e]), hk));
-      }
-    const float dv = (O::lo(vraw) - reduce(hk) * ks) * gt.y;
-    const float kd = dv * ks;
-    float hq = 0.f;
+        for (int e = 0; e < 2; ++e) {
+          const float k0 = O::lo(kr[c][e]), k1 = O::hi(kr[c][e]), q0 = O::lo(qr[c][e]), q1 = O::hi(qr[c][e]);
+          kk = fmaf(k0, k0, fmaf(k1, k1, kk));
+          qq = fmaf(q0, q0, fmaf(q1, q1, qq));
+        }
+      const float ks = 1.0f / sqrtf(reduce(kk) + 1e-6f), qs = a.scale / sqrtf(reduce(qq) + 1e-6f);  // (:147-150)
+      const float2 gt = gate_of(ga, gb, a.gate_dtype, 1.0f, 20.0f, A, dt_bias);
+      float hk = 0.f;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
+      for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float& h0 = h[8 * c + 2 * e];
-        float& h1 = h[8 * c + 2 * e + 1];
-        h0 = fmaf(O::lo(kr[c][e]), kd, h0);
-        h1 = fmaf(O::hi(kr[c][e]), kd, h1);
-        hq = fmaf(h0, O::lo(qr[c][e]), fmaf(h1, O::hi(qr[c][e]), hq));
-      }
-    hq = reduce(hq);
-    if (g == 0) e4::store_scalar(a.out, tok * a.stride_o + static_cast<int64_t>(hv) * a.V + row, a.out_dtype, hq * qs);
+        for (int e = 0; e < 2; ++e) {
+          float& h0 = h[4 * c + 2 * e];
+          float& h1 = h[4 * c + 2 * e + 1];
+          h0 *= gt.x;
+          h1 *= gt.x;
+          hk = fmaf(h0, O::lo(kr[c][e]), fmaf(h1, O::hi(kr[c][e]), hk));
+        }
+      const float dv = (O::lo(vraw) - reduce(hk) * ks) * gt.y;
+      const float kd = dv * ks;
+      float hq = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float& h0 = h[4 * c + 2 * e];
+          float& h1 = h[4 * c + 2 * e + 1];
+          h0 = fmaf(O::lo(kr[c][e]), kd, h0);
+          h1 = fmaf(O::hi(kr[c][e]), kd, h1);
+          hq = fmaf(h0, O::lo(qr[c][e]), fmaf(h1, O::hi(qr[c][e]), hq));
+        }
+      hq = reduce(hq);
+      if (g8 == 0)
+        static_cast<uint16_t*>(a.out)[tok * a.stride_o + static_cast<int64_t>(hv) * a.V + row] = O::narrow(hq * qs);
+    }
   }
 }
 
@@ -173,11 +185,13 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   __shared__ __align__(16) uint16_t s_k[WMAX][PITCH];
   __shared__ __align__(16) uint16_t s_q[WMAX][PITCH];
   __shared__ uint16_t s_v[WMAX][ROWS];
-  __shared__ float s_dv[WMAX][ROWS];
+  __shared__ float s_dv[WMAX][ROWS];   // per node and row: delta (the record's), read again by the node's children
+  __shared__ float s_oq[WMAX][ROWS];   // per node and row: decay qs (h~_parent q), the output less its delta term
   __shared__ float4 s_nd[WMAX];  // per node: decay ks, beta, decay qs, ks qs (k . q)
   __shared__ float2 s_gk[WMAX];  // per node: decay, ks
   __shared__ float2 s_g[WMAX];   // per node: decay, beta
   __shared__ int s_par[64];
+  __shared__ __align__(4) uint8_t s_ch[WMAX + 1][WMAX];  // row p + 1: the children of node p in order (0xff: none)
 
   // Work item: consecutive items share a request and key head; the hardware deals workgroups to the 8 XCDs in turn,
   // so item = (block % 8) * per_xcd + block / 8 gives each XCD a contiguous run.
@@ -189,7 +203,6 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
   const int row0 = tile * ROWS;
   const int wrow = wave * 16 + r16;            // the lane's row within the workgroup
-  const int row = row0 + wrow;                 // and within the head
   const bool wave_on = row0 + wave * 16 < a.V;  // V % 16 == 0: a wave's rows are all inside or all past V
 
   const int64_t bos = uni64(e4::ld(a.query_start_loc, n));
@@ -202,12 +215,12 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   const float A = -expf(widen_raw(A_raw, a.A_log_dtype));
   const float dt_bias = widen_raw(dt_raw, a.dt_bias_dtype);
   if (rec_row < 0) {  // a request without records never reloads a parent: one chain, no rounding
-    if (wave_on) chain_walk<K, T>(a, bos, T_, idx, hv, ih, row, g, A, dt_bias);
+    if (wave_on) chain_walk<K, T>(a, bos, T_, idx, hv, ih, row0 + wave * 16, lane, A, dt_bias);
     return;
   }
   const int Tn = T_ < a.width ? T_ : a.width;  // a tree has at most width (<= WMAX) rows
 
-  // ---- prologue: every load in flight before the first wait -----------------------------------------------------------
+  // ---- prologue: every load in flight before the first wait --------------------------------------------------------
   // the wave's 16 rows of the pool state in the operand layout, through a buffer resource that is empty for a negative
   // slot index (zeros: the zero initial state, :73-75) or a wave past V
   const char* h0_base = static_cast<const char*>(a.state) +
@@ -269,6 +282,7 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
 #pragma unroll
   for (int j = 0; j < PE_IT; ++j) path_entry(tid + j * NT, pL[j], ptok[j], pprev[j], pd[j]);
   if (tid < 64) s_par[tid] = -2;
+  for (int i = tid; i < (WMAX + 1) * WMAX / 4; i += NT) reinterpret_cast<uint32_t*>(&s_ch[0][0])[i] = ~0u;
   __syncthreads();
 
   // ---- staging ------------------------------------------------------------------------------------------------------
@@ -299,14 +313,35 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   if (tid < Tn) s_g[tid] = gate_of(ga, gb, a.gate_dtype, 1.0f, 20.0f, A, dt_bias);  // decay, beta (:115-140)
   __syncthreads();
 
-  // per node: |q|^2, |k|^2 and k . q over K (:147-150), LPN adjacent threads a node, each a contiguous run
+  // The tree in every wave: lane i holds node i's parent (-1 a root, -2 not in the tree) and its children. Wave 0 also
+  // lists every node's children in order (s_ch), so a lane finds the children it serves with one LDS read.
+  const int par = lane < Tn ? s_par[lane] : -2;
+  uint64_t kids = 0;
+  for (int i = 0; i < Tn; ++i) {
+    const uint64_t m = __ballot(par == i);
+    if (lane == i) kids = m;
+  }
+  const uint64_t roots = __ballot(par == -1);
+  const uint64_t internal = __ballot(kids != 0);
   {
-    constexpr int LPN = NT / WMAX;
+    const int src = par >= 0 ? par : lane;  // every lane takes part in the shuffles
+    const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(kids & 0xffffffffu), src));
+    const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(kids >> 32), src));
+    const uint64_t sib = par == -1 ? roots : (static_cast<uint64_t>(hi) << 32) | lo;
+    if (wave == 0 && par >= -1)
+      s_ch[par + 1][__builtin_popcountll(sib & ((1ull << lane) - 1))] = static_cast<uint8_t>(lane);
+  }
+
+  // per node: |q|^2, |k|^2 and k . q over K (:147-150), LPN0 adjacent threads a node, the first LPN of them each
+  // summing a contiguous run
+  {
+    constexpr int LPN0 = NT / WMAX;
+    constexpr int LPN = LPN0 < K / 4 ? LPN0 : K / 4;
     constexpr int PER = K / LPN;
-    static_assert(PER % 4 == 0 && LPN <= 16, "norm split");
-    const int t = tid / LPN, part = tid % LPN;
+    static_assert(PER % 4 == 0 && LPN0 <= 16, "norm split");
+    const int t = tid / LPN0, part = tid % LPN0;
     float qq = 0.f, kk = 0.f, kq = 0.f;
-    if (t < Tn) {
+    if (t < Tn && part < LPN) {
 #pragma unroll
       for (int c = 0; c < PER / 4; ++c) {
         const uint2 xk = *reinterpret_cast<const uint2*>(&s_k[t][part * PER + 4 * c]);
@@ -322,9 +357,9 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
         }
       }
     }
-    kk = e4::group_sum<LPN>(kk);
-    qq = e4::group_sum<LPN>(qq);
-    kq = e4::group_sum<LPN>(kq);
+    kk = e4::group_sum<LPN0>(kk);
+    qq = e4::group_sum<LPN0>(qq);
+    kq = e4::group_sum<LPN0>(kq);
     if (t < Tn && part == 0) {
       const float2 gt = s_g[t];
       const float ks = 1.0f / sqrtf(kk + 1e-6f), qs = a.scale / sqrtf(qq + 1e-6f);
@@ -349,62 +384,39 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
       }
     }
   }
-  if (!wave_on) return;
-
-  // ---- the tree: lane i holds node i's parent (-1 a root, -2 not in the tree) and children ---------------------------
-  const int par = lane < Tn ? s_par[lane] : -2;
-  uint64_t kids = 0;
-  for (int i = 0; i < Tn; ++i) {
-    const uint64_t m = __ballot(par == i);
-    if (lane == i) kids = m;
-  }
-  const uint64_t roots = __ballot(par == -1);
-  const uint64_t internal = __ballot(kids != 0);
-
-  const int64_t out_col = static_cast<int64_t>(hv) * a.V + row;
-
-  // All children in C of a node whose rounded state is Hc, eight at a time: one MFMA pass gives h~ k_j (rows 0-7 of
-  // the other operand) and h~ q_j (rows 8-15); lane (g, r16) receives element r of row 4 g + r for V row r16.
-  auto serve = [&](uint64_t C, const u32x4 (&Hc)[KB]) {
-    while (C != 0) {
-      // this pass: the lowest 8 children; the lane's operand row r16 holds child r16 % 8 (its k, or its q from row 8),
-      // its result elements children 4 (g % 2) + r
-      uint64_t m_op = C, m_res = C;
+  // ---- the tree walk (waves inside V): deltas and output terms gather in LDS, stored at the end --------------------
+  // The children of node u (-1: the roots) from its rounded state Hc, eight per pass: one MFMA pass gives h~ k_j
+  // (operand rows 0-7) and h~ q_j (rows 8-15); lane (g, r16) receives element r of row 4 g + r for V row r16, i.e.
+  // h~ k (g < 2) or h~ q (g >= 2) of child 4 (g % 2) + r of the pass.
+  auto serve = [&](int u, int nch, const u32x4 (&Hc)[KB]) {
+    for (int base = 0; base < nch; base += 8) {
+      const uint8_t* list = &s_ch[u + 1][base];
+      const int mine = list[r16 & 7];  // the child whose k (r16 < 8) or q this lane's operand row holds
+      const uint32_t cw = *reinterpret_cast<const uint32_t*>(list + 4 * (g & 1));  // the lane's 4 result children
+      int c[4];
+      float4 nd[4];
+      float vv[4];
 #pragma unroll
-      for (int e = 0; e < 7; ++e)
-        if (e < (r16 & 7)) m_op &= m_op - 1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (g & 1) m_res &= m_res - 1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) C &= C - 1;
-      const int mine = m_op != 0 ? static_cast<int>(__builtin_ctzll(m_op)) : -1;
-      const uint16_t* src = (r16 < 8 ? &s_k[0][0] : &s_q[0][0]) + (mine >= 0 ? mine : 0) * PITCH + g * KQ;
+      for (int r = 0; r < 4; ++r) {
+        const int x = (cw >> (8 * r)) & 0xff;
+        c[r] = x == 0xff ? -1 : x;
+        const int cc = x == 0xff ? 0 : x;
+        nd[r] = s_nd[cc];
+        vv[r] = O::lo(s_v[cc][wrow]);
+      }
+      const uint16_t* src = (r16 < 8 ? &s_k[0][0] : &s_q[0][0]) + (mine == 0xff ? 0 : mine) * PITCH + g * KQ;
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
         u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * kb);
-        if (mine < 0) x = u32x4{0u, 0u, 0u, 0u};
+        if (mine == 0xff) x = u32x4{0u, 0u, 0u, 0u};
         acc = O::mma(x, Hc[kb], acc);
       }
+      // lanes g < 2: delta = (v - decay ks h~ k) beta; lanes g >= 2: decay qs h~ q (the output less delta ks qs k.q)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int c = m_res != 0 ? static_cast<int>(__builtin_ctzll(m_res)) : -1;
-        m_res &= m_res - 1;
-        const int cc = c >= 0 ? c : 0;
-        const float4 nd = s_nd[cc];
-        const uint16_t vraw = s_v[cc][wrow];
-        const float dv = (O::lo(vraw) - nd.x * acc[r]) * nd.y;  // lanes g < 2: h~ k_j
-        const float dvx = __shfl(dv, lane ^ 32);
-        const float o = nd.z * acc[r] + dvx * nd.w;  // lanes g >= 2: h~ q_j
-        if (c >= 0) {
-          if (g < 2) {
-            s_dv[c][wrow] = dv;
-            rec[(static_cast<int64_t>(c) * a.HV + hv) * a.rec + row] = dv;
-          } else {
-            e4::store_scalar(a.out, (bos + c) * a.stride_o + out_col, a.out_dtype, o);
-          }
-        }
+        const float x = g < 2 ? (vv[r] - nd[r].x * acc[r]) * nd[r].y : nd[r].z * acc[r];
+        if (c[r] >= 0) (g < 2 ? s_dv : s_oq)[c[r]][wrow] = x;
       }
     }
     lds_order();
@@ -446,6 +458,7 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
     sid[0] = u;
     sp = sp < S ? sp + 1 : S;
   };
+  auto top_id = [&]() { return sp > 0 ? sid[0] : -3; };
   auto pop = [&]() {
 #pragma unroll
     for (int s = 0; s + 1 < S; ++s) {
@@ -458,7 +471,7 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   };
   // H <- the rounded state of node p (-1: the pool state): the stack's top, or its root path replayed
   auto restore = [&](int p) {
-    if (p >= 0 && sp > 0 && sid[0] == p) {
+    if (p >= 0 && top_id() == p) {
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) H[kb] = st[0][kb];
       return;
@@ -475,17 +488,16 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   };
 
   // Depth first over the internal nodes: serve a node's children, then step into its first child that has children
-  // of its own, or climb to the nearest ancestor with such a child left.
+  // of its own, or climb to the nearest ancestor with such a child left and take up that ancestor's state.
   int u = -1;
-  for (int it = 0; it <= Tn; ++it) {
+  for (int it = 0; wave_on && it <= Tn; ++it) {
     const uint64_t C = u < 0 ? roots : readlane64(kids, u);
-    serve(C, H);
+    serve(u, __builtin_popcountll(C), H);
     const uint64_t ik = C & internal;
     int j = -1;
     if (ik != 0) {
       j = static_cast<int>(__builtin_ctzll(ik));
       if (u >= 0 && (ik & (ik - 1)) != 0) push(u);  // more such children later: park the state
-      advance(H, j);
     } else {
       for (int x = u, hops = 0; x >= 0 && hops < 64; ++hops) {
         const int p = readlane(par, x);
@@ -494,15 +506,30 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
         if (sib != 0) {
           j = static_cast<int>(__builtin_ctzll(sib));
           restore(p);
-          if ((sib & (sib - 1)) == 0 && p >= 0 && sp > 0 && sid[0] == p) pop();  // its last one: unpark
-          advance(H, j);
+          if ((sib & (sib - 1)) == 0 && p >= 0 && top_id() == p) pop();  // its last one: unpark
           break;
         }
         x = p;
       }
     }
     if (j < 0) break;
+    advance(H, j);
     u = j;
+  }
+  __syncthreads();
+
+  // ---- every tree node's record delta and output, 4 rows a thread (:95-101) ----------------------------------------
+  uint16_t* const out = static_cast<uint16_t*>(a.out) + bos * a.stride_o + static_cast<int64_t>(hv) * a.V + row0;
+  for (int i = tid; i < Tn * (ROWS / 4); i += NT) {
+    const int t = i / (ROWS / 4), r = 4 * (i % (ROWS / 4));
+    if (s_par[t] == -2 || row0 + r >= a.V) continue;
+    const float4 dv = *reinterpret_cast<const float4*>(&s_dv[t][r]);
+    const float4 oq = *reinterpret_cast<const float4*>(&s_oq[t][r]);
+    const float w = s_nd[t].w;
+    *reinterpret_cast<float4*>(rec + (static_cast<int64_t>(t) * a.HV + hv) * a.rec + row0 + r) = dv;
+    const u32x2 o = {O::pack(fmaf(dv.x, w, oq.x), fmaf(dv.y, w, oq.y)),
+                     O::pack(fmaf(dv.z, w, oq.z), fmaf(dv.w, w, oq.w))};
+    *reinterpret_cast<u32x2*>(out + t * a.stride_o + r) = o;
   }
 }
 
@@ -529,14 +556,17 @@ int launch_w(const eagle4_records_args& a, hipStream_t s) {
 
 namespace e4replay {
 
-// The path replay on the matrix cores when it covers the call: a path table, 16-bit q / k / v and pool of one dtype
-// (the MFMA operands exact), a key dim of 32 .. 256 (a multiple of 32), a value dim that is a multiple of 16, trees of
-// <= 64 nodes, 16-byte aligned q / k rows and pool slots. Returns EAGLE4_NOT_COVERED (nothing launched) otherwise.
+// The path replay on the matrix cores when it covers the call: a path table, 16-bit q / k / v, output and pool of one
+// dtype (the MFMA operands exact), a key dim of 32 .. 256 (a multiple of 32), a value dim that is a multiple of 16,
+// trees of <= 64 nodes, 16-byte aligned q / k rows, pool slots and records, 8-byte aligned output rows. Returns
+// EAGLE4_NOT_COVERED (nothing launched) otherwise.
 int launch(const eagle4_records_args& a, hipStream_t s) {
   const auto al = [](const void* p, int64_t bytes) { return reinterpret_cast<uintptr_t>(p) % bytes == 0; };
-  if (!a.path_replay || a.in_dtype != a.state_dtype || (a.in_dtype != EAGLE4_BF16 && a.in_dtype != EAGLE4_F16) ||
+  if (!a.path_replay || a.in_dtype != a.state_dtype || a.out_dtype != a.in_dtype ||
+      (a.in_dtype != EAGLE4_BF16 && a.in_dtype != EAGLE4_F16) ||
       a.width < 1 || a.width > 64 || a.V % 16 || a.V < 16 || a.HV % a.H || a.rec < a.V + a.K + 1 || a.stride_q % 8 ||
-      a.stride_k % 8 || a.stride_state % 8 || !al(a.q, 16) || !al(a.k, 16) || !al(a.state, 16) ||
+      a.stride_k % 8 || a.stride_state % 8 || !al(a.q, 16) || !al(a.k, 16) || !al(a.state, 16) || a.rec % 4 ||
+      a.stride_records_row % 4 || !al(a.records, 16) || a.stride_o % 4 || !al(a.out, 8) ||
       a.tree_paths.dtype != EAGLE4_I32)
     return EAGLE4_NOT_COVERED;
   switch (a.K) {
