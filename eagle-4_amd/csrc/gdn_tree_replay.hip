@@ -185,6 +185,7 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   __shared__ __align__(16) uint16_t s_k[WMAX][PITCH];
   __shared__ __align__(16) uint16_t s_q[WMAX][PITCH];
   __shared__ uint16_t s_v[WMAX][ROWS];
+  __shared__ __align__(16) float s_kh[WMAX][K];  // per node: the normalised key k ks
   __shared__ float s_dv[WMAX][ROWS];   // per node and row: delta (the record's), read again by the node's children
   __shared__ float s_oq[WMAX][ROWS];   // per node and row: decay qs (h~_parent q), the output less its delta term
   __shared__ float4 s_nd[WMAX];  // per node: decay ks, beta, decay qs, ks qs (k . q)
@@ -360,9 +361,18 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
     kk = e4::group_sum<LPN0>(kk);
     qq = e4::group_sum<LPN0>(qq);
     kq = e4::group_sum<LPN0>(kq);
+    const float ks = 1.0f / sqrtf(kk + 1e-6f);
+    if (t < Tn && part < LPN) {  // the normalised key, fp32 (what the record keeps and the state update adds)
+#pragma unroll
+      for (int c = 0; c < PER / 4; ++c) {
+        const uint2 xk = *reinterpret_cast<const uint2*>(&s_k[t][part * PER + 4 * c]);
+        *reinterpret_cast<float4*>(&s_kh[t][part * PER + 4 * c]) =
+            make_float4(O::lo(xk.x) * ks, O::hi(xk.x) * ks, O::lo(xk.y) * ks, O::hi(xk.y) * ks);
+      }
+    }
     if (t < Tn && part == 0) {
       const float2 gt = s_g[t];
-      const float ks = 1.0f / sqrtf(kk + 1e-6f), qs = a.scale / sqrtf(qq + 1e-6f);
+      const float qs = a.scale / sqrtf(qq + 1e-6f);
       s_nd[t] = make_float4(gt.x * ks, gt.y, gt.x * qs, ks * qs * kq);
       s_gk[t] = make_float2(gt.x, ks);
     }
@@ -372,15 +382,12 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   float* const rec = a.records + static_cast<int64_t>(rec_row) * a.stride_records_row;
   // the records' normalised keys and decays, once per (node, value head): the first tile's workgroup
   if (tile == 0) {
-    for (int i = tid; i < Tn * (K / 2); i += NT) {
-      const int t = i / (K / 2), k2 = 2 * (i % (K / 2));
+    for (int i = tid; i < Tn * (K / 4); i += NT) {
+      const int t = i / (K / 4), k4 = 4 * (i % (K / 4));
       if (s_par[t] != -2) {
-        const float ks = s_gk[t].y;
-        const uint32_t x = *reinterpret_cast<const uint32_t*>(&s_k[t][k2]);
-        float* p = rec + (static_cast<int64_t>(t) * a.HV + hv) * a.rec + a.V + k2;
-        p[0] = O::lo(x) * ks;
-        p[1] = O::hi(x) * ks;
-        if (k2 == 0) p[K] = s_gk[t].x;
+        float* p = rec + (static_cast<int64_t>(t) * a.HV + hv) * a.rec + a.V + k4;
+        *reinterpret_cast<float4*>(p) = *reinterpret_cast<const float4*>(&s_kh[t][k4]);
+        if (k4 == 0) p[K] = s_gk[t].x;
       }
     }
   }
@@ -423,19 +430,19 @@ __global__ __launch_bounds__(NT) void gdn_replay_kernel(const eagle4_records_arg
   };
   // Hc <- round(decay_j Hc + k^_j delta_j^T): node j's rounded state from its parent's
   auto advance = [&](u32x4 (&Hc)[KB], int j) {
-    const float2 gk = s_gk[j];
-    const float aj = gk.y * s_dv[j][wrow];
-    const uint16_t* kp = &s_k[j][g * KQ];
+    const float decay = s_gk[j].x;
+    const float dv = s_dv[j][wrow];
+    const float* kp = &s_kh[j][g * KQ];
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) {
-      const u32x4 kx = *reinterpret_cast<const u32x4*>(kp + 8 * kb);
+      const float4 k0 = *reinterpret_cast<const float4*>(kp + 8 * kb);
+      const float4 k1 = *reinterpret_cast<const float4*>(kp + 8 * kb + 4);
+      const float kh[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
       uint32_t nw[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t hw = Hc[kb][e], kw = kx[e];
-        const float x0 = fmaf(O::lo(kw), aj, O::lo(hw) * gk.x);
-        const float x1 = fmaf(O::hi(kw), aj, O::hi(hw) * gk.x);
-        nw[e] = O::pack(x0, x1);
+        const uint32_t hw = Hc[kb][e];
+        nw[e] = O::pack(fmaf(kh[2 * e], dv, O::lo(hw) * decay), fmaf(kh[2 * e + 1], dv, O::hi(hw) * decay));
       }
       Hc[kb] = u32x4{nw[0], nw[1], nw[2], nw[3]};
     }
@@ -549,7 +556,11 @@ int launch_k(const eagle4_records_args& a, hipStream_t s) {
 
 template <int K, int S>
 int launch_w(const eagle4_records_args& a, hipStream_t s) {
-  return a.width <= 16 ? launch_k<K, 16, S>(a, s) : launch_k<K, 64, S>(a, s);
+  if (a.width <= 16) return launch_k<K, 16, S>(a, s);
+  if constexpr (K == 256)  // the staged rows of 64 nodes would not fit LDS: up to 32
+    return a.width <= 32 ? launch_k<K, 32, S>(a, s) : EAGLE4_NOT_COVERED;
+  else
+    return launch_k<K, 64, S>(a, s);
 }
 
 }  // namespace
@@ -558,7 +569,7 @@ namespace e4replay {
 
 // The path replay on the matrix cores when it covers the call: a path table, 16-bit q / k / v, output and pool of one
 // dtype (the MFMA operands exact), a key dim of 32 .. 256 (a multiple of 32), a value dim that is a multiple of 16,
-// trees of <= 64 nodes, 16-byte aligned q / k rows, pool slots and records, 8-byte aligned output rows. Returns
+// trees of <= 64 nodes (<= 32 at K = 256), 16-byte aligned q / k rows, pool slots and records, 8-byte aligned output rows. Returns
 // EAGLE4_NOT_COVERED (nothing launched) otherwise.
 int launch(const eagle4_records_args& a, hipStream_t s) {
   const auto al = [](const void* p, int64_t bytes) { return reinterpret_cast<uintptr_t>(p) % bytes == 0; };
