@@ -78,14 +78,14 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_records_walk_kernel(const eagl
   // The prologue issues every load before its first wait: the initial state (the request's pool slot, zeros for a
   // negative index, :73-75), the staged nodes' inputs, the parent table, then the path table.
   float h[RPT][E];
-  uint4 h0raw[RPT][NJ];
+  u32x4 h0raw[RPT][NJ];
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
   auto issue_h0 = [&]() {
 #pragma unroll
     for (int s = 0; s < RPT; ++s)
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        h0raw[s][j] = make_uint4(0u, 0u, 0u, 0u);  // zero bits: +0.0 in every dtype
+        h0raw[s][j] = u32x4{0u, 0u, 0u, 0u};  // zero bits: +0.0 in every dtype
         if (idx >= 0 && rows[s] < a.V)
           load_state_raw(a.state, idx * a.stride_state + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
                          a.state_dtype, h0raw[s][j]);

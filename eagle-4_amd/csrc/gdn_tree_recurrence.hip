@@ -99,12 +99,12 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   const int64_t idx = uni64(e4::ld(a.h0_indices, n, nacc - 1));
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
   float h[RPT][E];
-  uint4 h0raw[RPT][NJ];
+  u32x4 h0raw[RPT][NJ];
 #pragma unroll
   for (int s = 0; s < RPT; ++s)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      h0raw[s][j] = make_uint4(0u, 0u, 0u, 0u);  // zero bits: +0.0 in every dtype
+      h0raw[s][j] = u32x4{0u, 0u, 0u, 0u};  // zero bits: +0.0 in every dtype
       if (idx > a.pad_slot_id && rows[s] < a.V)
         load_state_raw(a.h0_source, idx * a.stride_h0_source + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
                        a.h0_dtype, h0raw[s][j]);

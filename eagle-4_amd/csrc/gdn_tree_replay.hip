@@ -36,8 +36,6 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
-// 16 bytes as a native vector: arrays of it stay in registers (arrays of the uint4 struct can land in scratch memory)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVES = 4;          // waves per workgroup
 constexpr int NT = 64 * WAVES;    // threads per workgroup
@@ -85,7 +83,6 @@ E4_DEV void lds_order() { __asm__ volatile("" ::: "memory"); }
 // A rare path, kept small in registers so it does not cost the tree walk occupancy: the wave's 16 rows in two halves
 // of 8, lane (g8, r8) holding row r8 of the half and K elements [g8 K / 8, (g8 + 1) K / 8), the raw q / k words
 // widened where they are used.
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 template <int K, typename T>
 E4_DEV void chain_walk(const eagle4_records_args& a, int64_t bos, int Tn, int idx, int hv, int ih, int row16,
                        int lane, float A, float dt_bias) {

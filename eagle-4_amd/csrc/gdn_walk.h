@@ -48,9 +48,14 @@ E4_DEV void load4_code(const void* base, int64_t off, int dtype, float* out) {
     load4<e4::F16>(static_cast<const uint16_t*>(base) + off, out);
 }
 
-// Four raw input values (q or k) as loaded: a float4 for fp32 inputs, four 16-bit values in a uint2 otherwise.
+// Native vectors: arrays of them stay in registers (arrays of HIP's float4 / uint4 structs can land in scratch memory).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Four raw input values (q or k) as loaded: 16 bytes of fp32, or four 16-bit values in 8 bytes.
 template <typename T>
-using Raw4 = typename std::conditional<sizeof(typename T::storage) == 4, float4, uint2>::type;
+using Raw4 = typename std::conditional<sizeof(typename T::storage) == 4, f32x4, u32x2>::type;
 
 template <typename T>
 E4_DEV void widen4(const Raw4<T>& r, float* out) {
@@ -129,16 +134,16 @@ namespace e4walk {
 // ---- a walk's prologue: every load issued before the first wait -------------------------------------------------
 // Four state values of a runtime dtype as raw bits (16 bytes of fp32, or 8 bytes of a 16-bit dtype in .x / .y),
 // widened later: a conversion next to each load would make every load wait for the one before.
-E4_DEV void load_state_raw(const void* base, int64_t off, int dtype, uint4& r) {
+E4_DEV void load_state_raw(const void* base, int64_t off, int dtype, u32x4& r) {
   if (dtype == EAGLE4_F32) {
-    r = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + off);
+    r = *reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + off);
   } else {
     const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
-    r = make_uint4(t.x, t.y, 0u, 0u);
+    r = u32x4{t.x, t.y, 0u, 0u};
   }
 }
 
-E4_DEV void widen_state_raw(const uint4& r, int dtype, float* out) {
+E4_DEV void widen_state_raw(const u32x4& r, int dtype, float* out) {
   if (dtype == EAGLE4_F32) {
     out[0] = __uint_as_float(r.x);
     out[1] = __uint_as_float(r.y);

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
 
   // a tile's K / V rows into registers: float4 e = tid + 256 i is key e / (D / 4), d 4 (e % (D / 4)); keys past the
   // split (or the draft rows) read the last valid one, masked later
-  float4 rk[TL::PER], rv[TL::PER];
+  f32x4_t rk[TL::PER], rv[TL::PER];  // native vectors: an array of them stays in registers
   auto load = [&](int tile) {
     const bool is_new = tile >= n_ctx;
 #pragma unroll
@@ -128,8 +128,8 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
           ks = kc + blk * a.stride_kb + sl * a.stride_ks;
           vs = vc + blk * a.stride_vb + sl * a.stride_vs;
         }
-        rk[i] = *reinterpret_cast<const float4*>(ks + d4);
-        rv[i] = *reinterpret_cast<const float4*>(vs + d4);
+        rk[i] = *reinterpret_cast<const f32x4_t*>(ks + d4);
+        rv[i] = *reinterpret_cast<const f32x4_t*>(vs + d4);
       }
     }
   };
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(64 * kTilesF) void verify_f32_kernel(const eagle4_a
       const int e = tid + 256 * i;
       if (e < TL::Q4) {
         const int kk = e / (D / 4), d4 = 4 * (e % (D / 4));
-        *reinterpret_cast<float4*>(sK + kk * TL::KP + d4) = rk[i];
+        *reinterpret_cast<f32x4_t*>(sK + kk * TL::KP + d4) = rk[i];
         sVt[(d4 + 0) * TL::VP + kk] = rv[i].x;
         sVt[(d4 + 1) * TL::VP + kk] = rv[i].y;
         sVt[(d4 + 2) * TL::VP + kk] = rv[i].z;
