@@ -142,8 +142,9 @@ def _row(us: float, nbytes: int | None = None, **extra) -> dict:
 def _rows(steps: int) -> dict:
     """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
     batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
-    attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, and the rounded records
-    path replay and commit. Algorithmic bytes count every element once."""
+    attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, the rounded records
+    path replay and commit, and vLLM's round commit (KV compaction, chainize). Algorithmic bytes count every element
+    once."""
     import math
 
     import numpy as np
@@ -197,6 +198,42 @@ def _rows(steps: int) -> dict:
     tail = torch.zeros(W + 1, dtype=torch.int64, device=dev)
     us = _time_graph(lambda: tree_tail_words(mask, committed, tail, W), steps)
     rows["a8_tail_words_w16"] = _row(us)
+
+    # next row (f) 2: vLLM's round commit at batch 64 x 16 rows — the accepted rows' KV (4 KV heads, D 256 bf16, K and
+    # V adjacent, page 16) moved in 4 full-attention layers, and chainize
+    from eagle_harness.vllm.round_commit import KvCompactor, chainize
+    from workloads import accept_paths
+
+    Bc, Wc, Hc, Dc, page, Lc = 64, 16, 4, 256, 16, 4
+    trees_c = [seeded_tree(rng, Wc) for _ in range(Bc)]
+    path_c, plen_c = accept_paths(trees_c, 7, Wc)
+    ctx_c = torch.tensor(rng.integers(1024, 8192, Bc), dtype=torch.int32)
+    blocks_per = [(int(c) + Wc + page - 1) // page for c in ctx_c]
+    max_b = max(blocks_per)
+    perm = torch.tensor(rng.permutation(sum(blocks_per)), dtype=torch.int32)
+    table_c = torch.zeros(Bc, max_b, dtype=torch.int32)
+    off = 0
+    for b, nb in enumerate(blocks_per):
+        table_c[b, :nb] = perm[off : off + nb]
+        off += nb
+    caches_c = [torch.empty(sum(blocks_per), Hc, page, 2 * Dc, dtype=torch.bfloat16, device=dev) for _ in range(Lc)]
+    qsl_c = torch.arange(0, Bc * Wc + 1, Wc, dtype=torch.int32, device=dev)
+    seq_c = (ctx_c + Wc).to(dev)
+    idx_c = torch.arange(Bc, dtype=torch.int32, device=dev)
+    compactor = KvCompactor(caches_c, [table_c.to(dev)] * Lc, [page] * Lc, dev)
+    path_d, plen_d = path_c.to(dev), plen_c.to(dev)
+    us = _time_graph(lambda: compactor.compact(idx_c, qsl_c, qsl_c, seq_c, path_d, plen_d), steps)
+    moved = sum(sum(1 for j in range(1, int(plen_c[b])) if int(path_c[b, j]) != j) for b in range(Bc))
+    rows["kv_compaction_b64x16_4layers"] = _row(us, moved * Lc * Hc * 2 * Dc * 2 * 2)
+    ids_c = torch.zeros(Bc * Wc, dtype=torch.int64, device=dev)
+    pos_c = torch.zeros_like(ids_c)
+    src_c = torch.arange(Bc * Wc, dtype=torch.int64, device=dev)
+    sampled_c = torch.zeros(Bc, Wc, dtype=torch.int64, device=dev)
+    us = _time_graph(lambda: chainize(ids_c, pos_c, src_c, idx_mapping=idx_c, query_start_loc=qsl_c,
+                                      cu_num_logits=qsl_c, seq_lens=seq_c, path=path_d, path_len=plen_d,
+                                      sampled=sampled_c, width=Wc), steps)
+    rows["chainize_b64x16"] = _row(us)
+    del caches_c
 
     # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
     for name, shape, fp8, dtype in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True, torch.bfloat16),

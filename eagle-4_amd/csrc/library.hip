@@ -19,6 +19,8 @@ extern "C" int64_t eagle4_args_size(int which) {
     case 10: return sizeof(eagle4_accept_tail_args);
     case 11: return sizeof(eagle4_compact_rows_args);
     case 12: return sizeof(eagle4_state_commit_args);
+    case 13: return sizeof(eagle4_compact_kv_args);
+    case 14: return sizeof(eagle4_chainize_args);
     default: return -1;
   }
 }

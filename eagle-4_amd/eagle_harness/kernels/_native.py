@@ -178,6 +178,21 @@ class StateCommitArgs(ctypes.Structure):
     )
 
 
+class CompactKvArgs(ctypes.Structure):
+    _fields_ = _fields(
+        "layer_ptrs:p table_ptrs:p table_strides:p table_block_sizes:p idx_mapping:t query_start_loc:t "
+        "cu_num_logits:t seq_lens:t path:t path_len:t stride_block:q stride_head:q stride_slot:q block_size:i dim:i "
+        "dtype:i num_reqs:i layers:i heads:i"
+    )
+
+
+class ChainizeArgs(ctypes.Structure):
+    _fields_ = _fields(
+        "idx_mapping:t query_start_loc:t cu_num_logits:t seq_lens:t path:t path_len:t sampled:t input_ids:p "
+        "positions:p src_rows:p input_ids_dtype:i positions_dtype:i src_rows_dtype:i rows:i num_reqs:i reserved:i"
+    )
+
+
 # entry name -> (args struct, index in eagle4_args_size)
 ENTRIES = {
     "eagle4_stage_tree": (StageTreeArgs, 0),
@@ -193,6 +208,8 @@ ENTRIES = {
     "eagle4_accept_tail": (AcceptTailArgs, 10),
     "eagle4_compact_rows": (CompactRowsArgs, 11),
     "eagle4_linear_state_commit": (StateCommitArgs, 12),
+    "eagle4_compact_kv": (CompactKvArgs, 13),
+    "eagle4_chainize": (ChainizeArgs, 14),
 }
 EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_version", "eagle4_args_size")
 

@@ -316,11 +316,55 @@ typedef struct eagle4_state_commit_args {
 } eagle4_state_commit_args;
 int eagle4_linear_state_commit(const eagle4_state_commit_args* args, void* stream);
 
+/* ---- vLLM round commit: vllm/round_commit.py:33-83 (_compact_kv_kernel, KvCompactor.compact) ----------------------- */
+/* The KV of the accepted rows of every verified tree moves to the chain slots context + j, in every given
+ * full-attention layer (one launch). A request is a verified tree when its query width is > 1 and equals its
+ * logits count (:26-29). */
+typedef struct eagle4_compact_kv_args {
+  const uint64_t* layer_ptrs;       /* [L] device array: each layer's KV cache base */
+  const uint64_t* table_ptrs;       /* [L] device array: each layer's [num_reqs, max_blocks] int32 block table */
+  const int64_t* table_strides;     /* [L] device array: the table's row stride (elements) */
+  const int32_t* table_block_sizes; /* [L] device array: tokens per block of the table */
+  eagle4_itab idx_mapping;          /* [R] state slot of each batch row */
+  eagle4_itab query_start_loc;      /* [R + 1] */
+  eagle4_itab cu_num_logits;        /* [R + 1] */
+  eagle4_itab seq_lens;             /* [R] */
+  eagle4_itab path;                 /* [state slots, W] accepted rows, root first */
+  eagle4_itab path_len;             /* [state slots] */
+  int64_t stride_block, stride_head, stride_slot; /* elements, of the cache as the attention backend views it */
+  int32_t block_size;               /* tokens per cache block */
+  int32_t dim;                      /* elements of one token and head: K then V, adjacent and contiguous */
+  int32_t dtype;                    /* EAGLE4_BF16 / EAGLE4_F16 */
+  int32_t num_reqs, layers, heads;
+} eagle4_compact_kv_args;
+int eagle4_compact_kv(const eagle4_compact_kv_args* args, void* stream);
+
+/* ---- vLLM round commit: vllm/round_commit.py:146-215 (_chainize_kernel, chainize) -------------------------------- */
+/* Rewrites a verified tree's rows for the draft's prefill: row j takes the hidden state of accepted row path[j]
+ * (src_rows), chain position context + j, and the sampled token j - 1 (rows 1 .. accepted - 1). */
+typedef struct eagle4_chainize_args {
+  eagle4_itab idx_mapping;     /* [R] */
+  eagle4_itab query_start_loc; /* [R + 1] */
+  eagle4_itab cu_num_logits;   /* [R + 1] */
+  eagle4_itab seq_lens;        /* [R] */
+  eagle4_itab path;            /* [state slots, W] */
+  eagle4_itab path_len;        /* [state slots] */
+  eagle4_itab sampled;         /* [R, >= W - 1] sampled tokens in path order */
+  void* input_ids;             /* [tokens], in / out, dtype input_ids_dtype (EAGLE4_I32 / EAGLE4_I64) */
+  void* positions;             /* [tokens], in / out, dtype positions_dtype */
+  void* src_rows;              /* [tokens], in / out, dtype src_rows_dtype */
+  int32_t input_ids_dtype, positions_dtype, src_rows_dtype;
+  int32_t rows;                /* rows handled per request: the power of two >= the stage width (<= 64) */
+  int32_t num_reqs;
+  int32_t reserved;
+} eagle4_chainize_args;
+int eagle4_chainize(const eagle4_chainize_args* args, void* stream);
+
 /* ---- library introspection ---------------------------------------------------------------------------------------- */
 const char* eagle4_version(void);
 /* sizeof() of argument struct `which` (0 stage, 1 ancestors, 2 tail words, 3 conv, 4 gdn, 5 records, 6 records commit,
- * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit); -1 past the end. The host
- * binding checks its struct mirrors against these. */
+ * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit, 13 compact kv,
+ * 14 chainize); -1 past the end. The host binding checks its struct mirrors against these. */
 int64_t eagle4_args_size(int which);
 
 #ifdef __cplusplus
