@@ -143,8 +143,8 @@ def _rows(steps: int) -> dict:
     """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
     batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
     attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, the rounded records
-    path replay and commit, and vLLM's round commit (KV compaction, chainize). Algorithmic bytes count every element
-    once."""
+    path replay and commit, vLLM's round commit (KV compaction, chainize) and draft-row attention. Algorithmic bytes
+    count every element once."""
     import math
 
     import numpy as np
@@ -234,6 +234,29 @@ def _rows(steps: int) -> dict:
                                       sampled=sampled_c, width=Wc), steps)
     rows["chainize_b64x16"] = _row(us)
     del caches_c
+
+    # next row (f) 3: draft-row attention, a draft step (4 frontier rows, step 7) at batch 64 over a 4096-key window of
+    # 8192 committed keys, 32 query / 8 KV heads, D 128 bf16, slot-major cache through a permuted token table
+    from eagle_harness.kernels.row_attention import RowsLaunch, rows_attention, rows_padded
+
+    Br, rr, stp, win, Lr, Hq, Hk, Dr = 64, 4, 7, 4096, 8192, 32, 8, 128
+    nslot = Br * (Lr + rr * stp)
+    k_r = torch.randn(nslot, Hk, Dr, device=dev, generator=gen).bfloat16()
+    v_r = torch.randn(nslot, Hk, Dr, device=dev, generator=gen).bfloat16()
+    tab_r = torch.randperm(nslot, device=dev, generator=gen).to(torch.int32).view(Br, Lr + rr * stp)
+    anc_r = tab_r[:, Lr:].reshape(Br, rr, stp).contiguous()
+    q_r = torch.randn(Br * rr, Hq, Dr, device=dev, generator=gen).bfloat16()
+    out_r = torch.empty_like(q_r)
+    sp = 8
+    npart = Br * Hq * (sp + 1) * rows_padded(rr)
+    po, pl = torch.empty(npart, Dr, device=dev), torch.empty(npart, device=dev)
+    seq_r = torch.full((Br,), Lr, dtype=torch.int32, device=dev)
+    us = _time_graph(lambda: rows_attention(q_r, k_r, v_r, out_r, po, pl, tab_r, seq_r, anc_r, rows_per_request=rr,
+                                            step=stp, window=win, scale=Dr**-0.5,
+                                            launch=RowsLaunch(splits=sp, block_n=32)), steps)
+    rows["row_attention_step7_b64_window4096_d128"] = _row(us, Br * Hk * (win + rr * stp) * Dr * 2 * 2
+                                                           + Br * (win + rr * stp) * 4 + 2 * q_r.numel() * 2)
+    del k_r, v_r
 
     # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
     for name, shape, fp8, dtype in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True, torch.bfloat16),

@@ -106,10 +106,24 @@ struct Tile {
 //   B operand and V^T read by transposing LDS loads (ds_read_b64_tr_b16) of the row-major tile.
 // The reference's step is kernels/online_softmax.py:11-24 (max, rescale, exp, sum) over vllm/verify_attention.py
 // :62-112's masked scores.
+// tile_step_if takes the visibility as a predicate ok(key of the tile) of the lane's row.
+template <int D, typename T, typename Ok>
+E4_DEV void tile_step_if(const char* sKb, const char* sVb, const uint4 (&qreg)[D / 32], f32x4_t (&acc)[D / 16],
+                         float& m, float& l, float scale_log2, int g, int l16, Ok ok);
+
 template <int D, typename T>
 E4_DEV void tile_step(const char* sKb, const char* sVb, const uint4 (&qreg)[D / 32], f32x4_t (&acc)[D / 16], float& m,
                       float& l, float scale_log2, bool is_new, int base, int hi, int width, int64_t row_mask, int g,
                       int l16) {
+  tile_step_if<D, T>(sKb, sVb, qreg, acc, m, l, scale_log2, g, l16, [&](int k) {
+    const int key = base + k;
+    return is_new ? (key < width && ((row_mask >> key) & 1)) : key < hi;
+  });
+}
+
+template <int D, typename T, typename Ok>
+E4_DEV void tile_step_if(const char* sKb, const char* sVb, const uint4 (&qreg)[D / 32], f32x4_t (&acc)[D / 16],
+                         float& m, float& l, float scale_log2, int g, int l16, Ok ok) {
   using TL = Tile<D>;
   f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -125,9 +139,7 @@ E4_DEV void tile_step(const char* sKb, const char* sVb, const uint4 (&qreg)[D / 
   for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = base + 16 * kt + 4 * g + i;
-      const bool ok = is_new ? (key < width && ((row_mask >> key) & 1)) : key < hi;
-      const float v = ok ? s[kt][i] * scale_log2 : -INFINITY;
+      const float v = ok(16 * kt + 4 * g + i) ? s[kt][i] * scale_log2 : -INFINITY;
       s[kt][i] = v;
       tmax = fmaxf(tmax, v);
     }

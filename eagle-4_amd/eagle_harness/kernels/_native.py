@@ -193,6 +193,15 @@ class ChainizeArgs(ctypes.Structure):
     )
 
 
+class RowAttnArgs(ctypes.Structure):
+    _fields_ = _fields(
+        "q:p stride_q_row:q stride_q_head:q keys:p values:p k_stride_page:q k_stride_slot:q k_stride_head:q "
+        "v_stride_page:q v_stride_slot:q v_stride_head:q out:p stride_o_row:q stride_o_head:q part_out:p part_lse:p "
+        "part_rows:q table:p stride_table:q table_rows:t seq_lens:t ancestors:p max_depth:i table_page:i cache_page:i "
+        "bs:i rows_per_request:i rows_padded:i heads:i kv_heads:i head_dim:i dtype:i step:i window:i splits:i scale:f"
+    )
+
+
 # entry name -> (args struct, index in eagle4_args_size)
 ENTRIES = {
     "eagle4_stage_tree": (StageTreeArgs, 0),
@@ -210,6 +219,7 @@ ENTRIES = {
     "eagle4_linear_state_commit": (StateCommitArgs, 12),
     "eagle4_compact_kv": (CompactKvArgs, 13),
     "eagle4_chainize": (ChainizeArgs, 14),
+    "eagle4_row_attention": (RowAttnArgs, 15),
 }
 EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_version", "eagle4_args_size")
 

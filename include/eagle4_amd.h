@@ -360,11 +360,42 @@ typedef struct eagle4_chainize_args {
 } eagle4_chainize_args;
 int eagle4_chainize(const eagle4_chainize_args* args, void* stream);
 
+/* ---- draft-row attention: kernels/row_attention.py:96-328 (_rows_attention_kernel, _merge_splits_kernel) -------- */
+/* Rows of a draft step (step > 0: every row sees the committed window ending at seq_len - 1 plus its own `step`
+ * ancestors) or extend rows (step == 0: row j at seq_len + j sees its causal window). The key at position p of request
+ * b is slot table[table_rows[b] (or b), p / table_page] * table_page + p % table_page, at (slot / cache_page,
+ * slot % cache_page, KV head) of the caches. Partials go to the caller's scratch (part_rows rows of head_dim fp32 and
+ * one fp32 each) at ((b * heads + head) * (splits + 1) + split) * rows_padded + row; a second launch merges them. */
+typedef struct eagle4_row_attn_args {
+  const void* q;                 /* [bs * rows_per_request, heads, head_dim] */
+  int64_t stride_q_row, stride_q_head;
+  const void* keys;              /* cache view [pages, page, kv_heads, D] or [slots, kv_heads, D] (page 1) */
+  const void* values;            /* same; null: `keys` rows hold K then V (last dim 2 D) */
+  int64_t k_stride_page, k_stride_slot, k_stride_head; /* elements */
+  int64_t v_stride_page, v_stride_slot, v_stride_head;
+  void* out;                     /* like q */
+  int64_t stride_o_row, stride_o_head;
+  float* part_out;               /* [part_rows, head_dim] scratch */
+  float* part_lse;               /* [part_rows] scratch (log2 domain) */
+  int64_t part_rows;
+  const int32_t* table;          /* page table, a row per request (or per table_rows entry) */
+  int64_t stride_table;
+  eagle4_itab table_rows;        /* [bs] or null: row b */
+  eagle4_itab seq_lens;          /* [bs] committed lengths */
+  const int32_t* ancestors;      /* [bs, rows_per_request, max_depth] contiguous KV slots (step > 0) */
+  int32_t max_depth;
+  int32_t table_page, cache_page;
+  int32_t bs, rows_per_request, rows_padded, heads, kv_heads, head_dim, dtype;
+  int32_t step, window, splits;  /* window <= 0: the whole context; splits: key splits of the shared range */
+  float scale;
+} eagle4_row_attn_args;
+int eagle4_row_attention(const eagle4_row_attn_args* args, void* stream);
+
 /* ---- library introspection ---------------------------------------------------------------------------------------- */
 const char* eagle4_version(void);
 /* sizeof() of argument struct `which` (0 stage, 1 ancestors, 2 tail words, 3 conv, 4 gdn, 5 records, 6 records commit,
  * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit, 13 compact kv,
- * 14 chainize); -1 past the end. The host binding checks its struct mirrors against these. */
+ * 14 chainize, 15 row attention); -1 past the end. The host binding checks its struct mirrors against these. */
 int64_t eagle4_args_size(int which);
 
 #ifdef __cplusplus
