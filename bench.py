@@ -143,7 +143,8 @@ def _rows(steps: int) -> dict:
     """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
     batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
     attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, the rounded records
-    path replay and commit, vLLM's round commit (KV compaction, chainize) and draft-row attention. Algorithmic bytes
+    path replay and commit, vLLM's round commit (KV compaction, chainize), draft-row attention and the GDN layer front
+    on projection views. Algorithmic bytes
     count every element once."""
     import math
 
@@ -257,6 +258,34 @@ def _rows(steps: int) -> dict:
     rows["row_attention_step7_b64_window4096_d128"] = _row(us, Br * Hk * (win + rr * stp) * Dr * 2 * 2
                                                            + Br * (win + rr * stp) * 4 + 2 * q_r.numel() * 2)
     del k_r, v_r
+
+    # next row (f) 1: the GDN layer front at the step's layer (B64 T16, H16/HV32, K = V = 128, fp32 states): the conv
+    # and the walk reading token-strided views of one [qkv | z | b | a] projection buffer, no split or copy kernels
+    from types import SimpleNamespace
+
+    from eagle_harness.vllm.gdn_tree_verify import GDNSpecRows, TreeVerify
+    from eagle_harness.vllm.verify_layout import set_stage
+    from workloads import GDN_B64
+
+    g = gdn_inputs(GDN_B64, seed=4, device=dev, layout="vllm", gen_device=dev)
+    Bf, Wf, H, HV, K, V = GDN_B64.batch, GDN_B64.width, GDN_B64.h, GDN_B64.hv, GDN_B64.k, GDN_B64.v
+    tokens, dim = Bf * Wf, g["dim"]
+    proj = torch.randn(tokens, dim + HV * V + 2 * HV, device=dev, generator=gen).bfloat16()
+    front_rows = GDNSpecRows("layers.0.linear_attn", proj[:, :dim], g["conv_state"], g["conv_weight"], None, "silu",
+                             proj[:, dim + HV * V + HV :], proj[:, dim + HV * V : dim + HV * V + HV], g["A_log"],
+                             g["dt_bias"], g["pool"], g["slots"], g["query_start_loc"], g["num_accepted"],
+                             torch.empty(tokens, HV * V, dtype=torch.bfloat16, device=dev), H, K, HV, V)
+    set_stage(SimpleNamespace(ancestors=g["ancestors"], parents=g["parent_table"], state_slots={}))
+    try:
+        us = _time_graph(lambda: TreeVerify().forward_spec_rows(front_rows), steps)
+    finally:
+        set_stage(None)
+    state = HV * K * V * 4
+    conv_b = tokens * dim * 2 * 2 + Bf * dim * 3 * 2 + Bf * dim * (Wf + 2) * 2 + dim * 4 * 2
+    rec_b = (Bf * state + tokens * state + tokens * H * K * 2 * 2 + tokens * HV * V * 2 + tokens * HV * 2 * 2
+             + tokens * HV * V * 2 + tokens * 4)
+    rows["gdn_front_views_b64x16"] = _row(us, conv_b + rec_b)
+    del g, proj, front_rows
 
     # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
     for name, shape, fp8, dtype in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True, torch.bfloat16),

@@ -1,4 +1,5 @@
-"""Accepted-path commit of the linear-attention state for vLLM hybrid targets (vllm/gdn_tree_verify.py:184-322),
+"""The GDN layer's tree-verify front (``TreeVerify.forward_spec_rows``, vllm/gdn_tree_verify.py:55-106) and the
+accepted-path commit of the linear-attention state (vllm/gdn_tree_verify.py:184-322) for vLLM hybrid targets,
 engine-free.
 
 vLLM keeps one recurrent-state slot per verify row (``slots[b, i]``) and the request's conv window in slot
@@ -11,11 +12,15 @@ layers move in one gfx950 launch per kind (``csrc/state_commit.hip``).
 from __future__ import annotations
 
 from collections.abc import Sequence
+from dataclasses import dataclass
 from typing import Any
 
 import torch
 
 from eagle_harness.kernels import _native
+from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
+from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+from eagle_harness.vllm.verify_layout import get_stage
 
 # A padded request's state slot (vLLM's null block); the chain kernels skip it too.
 NULL_BLOCK_ID = 0
@@ -83,3 +88,94 @@ class LinearStateCommit:
             dim=self.dim,
         )
         _native.launch("eagle4_linear_state_commit", args, self.device)
+
+
+@dataclass
+class GDNSpecRows:
+    """The speculative-decode rows a Qwen GDN layer hands its verify extension (vLLM's ``GDNSpecRows``, the fields
+    vllm/gdn_tree_verify.py:65-106 reads). ``mixed_qkv`` ``[tokens, 2 H K + HV V]``, ``a`` / ``b`` ``[tokens, HV]``
+    may be token-strided views of the layer's input projection; ``out`` ``[tokens, HV V]`` receives the recurrence
+    output."""
+
+    layer_name: str
+    mixed_qkv: torch.Tensor
+    conv_state: torch.Tensor
+    conv_weight: torch.Tensor
+    conv_bias: torch.Tensor | None
+    activation: str | None
+    a: torch.Tensor
+    b: torch.Tensor
+    A_log: torch.Tensor
+    dt_bias: torch.Tensor
+    ssm_state: torch.Tensor
+    state_indices: torch.Tensor
+    query_start_loc: torch.Tensor
+    num_accepted_tokens: torch.Tensor
+    out: torch.Tensor
+    num_k_heads: int
+    head_k_dim: int
+    num_v_heads: int
+    head_v_dim: int
+
+
+class TreeVerify:
+    """A GDN layer's tree-verify front (vllm/gdn_tree_verify.py:55-106): the tree conv over the layer's qkv projection,
+    then the tree recurrence on q / k / v views of the conv output and a / b views of the projection. No split or copy
+    kernel sits between the input projection's GEMM and the conv, nor between the conv and the recurrence: both gfx950
+    kernels address token-strided inputs, and on one stream the conv starts as the GEMM ends."""
+
+    def __init__(self, vllm_config: Any = None):
+        self.vllm_config = vllm_config
+
+    def forward_spec_rows(self, rows: GDNSpecRows) -> None:
+        stage = _staged()
+        tokens, dim = rows.mixed_qkv.shape
+        conv = torch.empty(tokens, dim, dtype=rows.mixed_qkv.dtype, device=rows.mixed_qkv.device)
+        gdn_tree_conv1d_update(
+            rows.mixed_qkv.t()[None],
+            rows.conv_state,
+            rows.conv_weight,
+            rows.conv_bias,
+            rows.activation,
+            conv_state_indices=rows.state_indices[:, 0],
+            intermediate_conv_window=None,
+            intermediate_state_indices=None,
+            tree_ancestors=stage.ancestors[: rows.query_start_loc.shape[0] - 1],
+            pad_slot_id=NULL_BLOCK_ID,
+            out=conv.t()[None],
+            num_accepted_tokens=rows.num_accepted_tokens,
+            query_start_loc=rows.query_start_loc,
+        )
+        key_dim = rows.num_k_heads * rows.head_k_dim
+        q, k, v = conv.split([key_dim, key_dim, rows.num_v_heads * rows.head_v_dim], dim=-1)
+        published = getattr(stage, "state_slots", {}).get(rows.layer_name)
+        gdn_tree_recurrent_update(
+            rows.A_log,
+            rows.dt_bias,
+            q.view(1, tokens, -1, rows.head_k_dim),
+            k.view(1, tokens, -1, rows.head_k_dim),
+            v.view(1, tokens, -1, rows.head_v_dim),
+            rows.a,
+            rows.b,
+            initial_state_source=rows.ssm_state,
+            initial_state_indices=rows.state_indices,
+            num_accepted_tokens=rows.num_accepted_tokens,
+            cu_seqlens=rows.query_start_loc,
+            intermediate_states_buffer=rows.ssm_state,
+            intermediate_state_indices=rows.state_indices,
+            retrieve_parent_token=stage.parents,
+            pad_slot_id=NULL_BLOCK_ID,
+            out=rows.out.view(1, tokens, -1, rows.head_v_dim),
+            publish=None if published is None else published[: rows.state_indices.shape[0]],
+            gluon=True,
+        )
+
+    def forward_mamba2_spec_rows(self, rows: Any) -> None:
+        raise _native.NotCovered("the Mamba2 tree state update has no gfx950 kernel in this library")
+
+
+def _staged() -> Any:
+    stage = get_stage()
+    if stage is None:
+        raise RuntimeError("eagle_harness: a linear-attention verify ran before the speculator staged its layout")
+    return stage

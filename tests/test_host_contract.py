@@ -33,3 +33,15 @@ def test_fp8_cache_needs_its_scales():
         verify_attention(q, q, q, cache, cache, torch.zeros(1, 2, dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
                          torch.tensor([0, 1], dtype=torch.int32), torch.ones(1, 1, dtype=torch.int64), 1.0, q,
                          max_query_len=1)
+
+
+def test_front_without_a_stage_refuses():
+    """A verify before the speculator staged its tables is an error, as in the reference (:169-173)."""
+    from types import SimpleNamespace
+
+    from eagle_harness.vllm.gdn_tree_verify import TreeVerify
+    from eagle_harness.vllm.verify_layout import set_stage
+
+    set_stage(None)
+    with pytest.raises(RuntimeError, match="staged"):
+        TreeVerify().forward_spec_rows(SimpleNamespace())
