@@ -143,8 +143,8 @@ def _rows(steps: int) -> dict:
     """The rows and configurations the step does not contain, each timed like the step's parts: the accept path at
     batch 512 x 16 over a 151936-token vocab (argmax, tree walk), the bs1 accept tail, the tail-mask words, fp8 verify
     attention at batch 512, the GDN walk at batch 1 and 256, fp32 and bf16 attention at batch 1, the rounded records
-    path replay and commit, vLLM's round commit (KV compaction, chainize), draft-row attention and the GDN layer front
-    on projection views. Algorithmic bytes
+    path replay and commit, vLLM's round commit (KV compaction, chainize), draft-row attention, the GDN layer front
+    on projection views and the Mamba2 tree state update. Algorithmic bytes
     count every element once."""
     import math
 
@@ -286,6 +286,30 @@ def _rows(steps: int) -> dict:
              + tokens * HV * V * 2 + tokens * 4)
     rows["gdn_front_views_b64x16"] = _row(us, conv_b + rec_b)
     del g, proj, front_rows
+
+    # next row (f) 4: the Mamba2 tree state update at Nemotron 3 Nano's TP1 layer (64 heads x 64 x 128 state, 8
+    # groups, fp32 state pool), batch 64 x 16-node seeded trees, one state slot per row
+    from eagle_harness.kernels.mamba2_tree import mamba2_tree_state_update
+
+    Bm, Wm, Hm, Pm, Gm, Nm = 64, 16, 64, 64, 8, 128
+    tm = Bm * Wm
+    rng_m = np.random.default_rng(8)
+    par_m = torch.tensor([seeded_tree(rng_m, Wm) for _ in range(Bm)], dtype=torch.int32, device=dev)
+    slots_m = (1 + torch.arange(Bm * Wm, dtype=torch.int32, device=dev)).view(Bm, Wm)
+    st_m = torch.randn(1 + Bm * Wm, Hm, Pm, Nm, device=dev, generator=gen) * 0.1
+    x_m = torch.randn(tm, Hm, Pm, device=dev, generator=gen).bfloat16()
+    dt_m = torch.randn(tm, Hm, device=dev, generator=gen).bfloat16()
+    bc_m = torch.randn(tm, 2, Gm, Nm, device=dev, generator=gen).bfloat16()
+    A_m, D_m, bias_m = -torch.rand(Hm, device=dev), torch.randn(Hm, device=dev), torch.randn(Hm, device=dev)
+    o_m = torch.empty_like(x_m)
+    qsl_m = torch.arange(0, tm + 1, Wm, dtype=torch.int32, device=dev)
+    us = _time_graph(lambda: mamba2_tree_state_update(st_m, x_m, dt_m, A_m, bc_m[:, 0], bc_m[:, 1], D_m, bias_m, o_m,
+                                                      state_indices=slots_m, parents=par_m, query_start_loc=qsl_m),
+                     steps)
+    state_m = Hm * Pm * Nm * 4
+    rows["mamba2_tree_b64x16_nano_tp1"] = _row(us, Bm * state_m + tm * state_m + tm * (2 * Hm * Pm * 2 + 2 * Gm * Nm * 2
+                                                                                      + Hm * 2 + 8))
+    del st_m
 
     # a6: fp8-e4m3 pages with per-(page, KV head) scales at batch 512 (Hq24/Hkv4, D256, prefixes U[512, 4096])
     for name, shape, fp8, dtype in (("a6_attention_fp8_b512_d256", ATTN_B512_FP8, True, torch.bfloat16),

@@ -22,6 +22,7 @@ extern "C" int64_t eagle4_args_size(int which) {
     case 13: return sizeof(eagle4_compact_kv_args);
     case 14: return sizeof(eagle4_chainize_args);
     case 15: return sizeof(eagle4_row_attn_args);
+    case 16: return sizeof(eagle4_mamba2_args);
     default: return -1;
   }
 }

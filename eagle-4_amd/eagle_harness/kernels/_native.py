@@ -203,6 +203,16 @@ class RowAttnArgs(ctypes.Structure):
 
 
 # entry name -> (args struct, index in eagle4_args_size)
+class Mamba2Args(ctypes.Structure):
+    _fields_ = _fields(
+        "state:p stride_state_slot:q stride_state_head:q stride_state_dim:q x:p stride_x_tok:q stride_x_head:q dt:p "
+        "stride_dt_tok:q stride_dt_head:q B:p stride_B_tok:q stride_B_group:q C:p stride_C_tok:q stride_C_group:q A:p "
+        "D:p dt_bias:p out:p stride_out_tok:q stride_out_head:q slots:t parents:t num_accepted:t query_start_loc:t "
+        "batch:i heads:i head_dim:i dstate:i groups:i state_dtype:i in_dtype:i dt_dtype:i param_dtype:i out_dtype:i "
+        "dt_softplus:i pad_slot_id:i"
+    )
+
+
 ENTRIES = {
     "eagle4_stage_tree": (StageTreeArgs, 0),
     "eagle4_gdn_tree_ancestors": (AncestorsArgs, 1),
@@ -220,6 +230,7 @@ ENTRIES = {
     "eagle4_compact_kv": (CompactKvArgs, 13),
     "eagle4_chainize": (ChainizeArgs, 14),
     "eagle4_row_attention": (RowAttnArgs, 15),
+    "eagle4_mamba2_tree_state_update": (Mamba2Args, 16),
 }
 EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_version", "eagle4_args_size")
 

@@ -395,8 +395,43 @@ int eagle4_row_attention(const eagle4_row_attn_args* args, void* stream);
 const char* eagle4_version(void);
 /* sizeof() of argument struct `which` (0 stage, 1 ancestors, 2 tail words, 3 conv, 4 gdn, 5 records, 6 records commit,
  * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit, 13 compact kv,
- * 14 chainize, 15 row attention); -1 past the end. The host binding checks its struct mirrors against these. */
+ * 14 chainize, 15 row attention, 16 mamba2); -1 past the end. The host binding checks its struct mirrors against these. */
 int64_t eagle4_args_size(int which);
+
+/* ---- Mamba2 tree state update: kernels/mamba2_tree.py:41-240 (_tree_ssu_kernel, mamba2_tree_state_update) ------ */
+/* Request b's rows are tokens query_start_loc[b] .. query_start_loc[b + 1] - 1. Row t continues from row
+ * parents[b, t] (row 0: the state at slots[b, max(num_accepted[b] - 1, 0)], column 0 without num_accepted): a row
+ * whose parent is t - 1 from the unrounded state, any other from its parent's stored slot. Every row stores its state
+ * at slots[b, t]; a slot equal to pad_slot_id reads as zeros and is never written.
+ *   state_t = exp(A dt_t) state_parent + (dt_t B_t) x_t,  dt_t = softplus(dt + dt_bias) (when dt_softplus),
+ *   out[t] = C_t . state_t + D x_t.
+ * dstate 64, 128 or 256; state, B and C with a unit stride over dstate and 4-element-aligned strides. */
+typedef struct eagle4_mamba2_args {
+  void* state;                  /* [slots, heads, head_dim, dstate], dtype state_dtype */
+  int64_t stride_state_slot, stride_state_head, stride_state_dim;
+  const void* x;                /* [tokens, heads, head_dim], dtype in_dtype, unit stride over head_dim */
+  int64_t stride_x_tok, stride_x_head;
+  const void* dt;               /* [tokens, heads], dtype dt_dtype */
+  int64_t stride_dt_tok, stride_dt_head;
+  const void* B;                /* [tokens, groups, dstate], dtype in_dtype */
+  int64_t stride_B_tok, stride_B_group;
+  const void* C;                /* like B */
+  int64_t stride_C_tok, stride_C_group;
+  const float* A;               /* [heads] fp32 (-exp(A_log)) */
+  const void* D;                /* [heads] or null, dtype param_dtype */
+  const void* dt_bias;          /* [heads] or null, dtype param_dtype */
+  void* out;                    /* like x, dtype out_dtype */
+  int64_t stride_out_tok, stride_out_head;
+  eagle4_itab slots;            /* [batch, >= rows] state slot of each row */
+  eagle4_itab parents;          /* [>= batch, rows] parent row of each row (row 0: -1) */
+  eagle4_itab num_accepted;     /* [batch] or absent */
+  eagle4_itab query_start_loc;  /* [batch + 1] */
+  int32_t batch, heads, head_dim, dstate, groups;
+  int32_t state_dtype, in_dtype, dt_dtype, param_dtype, out_dtype;
+  int32_t dt_softplus;
+  int32_t pad_slot_id;
+} eagle4_mamba2_args;
+int eagle4_mamba2_tree_state_update(const eagle4_mamba2_args* args, void* stream);
 
 #ifdef __cplusplus
 }
