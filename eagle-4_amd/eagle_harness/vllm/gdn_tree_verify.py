@@ -20,6 +20,7 @@ import torch
 from eagle_harness.kernels import _native
 from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
 from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+from eagle_harness.kernels.mamba2_tree import mamba2_tree_state_update
 from eagle_harness.vllm.verify_layout import get_stage
 
 # A padded request's state slot (vLLM's null block); the chain kernels skip it too.
@@ -171,7 +172,51 @@ class TreeVerify:
         )
 
     def forward_mamba2_spec_rows(self, rows: Any) -> None:
-        raise _native.NotCovered("the Mamba2 tree state update has no gfx950 kernel in this library")
+        """A Mamba2 layer's decode rows (vllm/gdn_tree_verify.py:107-148): the tree conv over ``hidden_states_B_C``,
+        then the tree selective state update on x / B / C views of the conv output. ``rows`` carries vLLM's
+        ``Mamba2SpecRows`` fields (hidden_states_B_C, conv_state, conv_weight, conv_bias, activation, state_indices,
+        query_start_loc, num_accepted_tokens, num_heads, head_dim, n_groups, ssm_state_size, ssm_state, dt, A, D,
+        dt_bias, out, layer_name)."""
+        stage = _staged()
+        tokens, dim = rows.hidden_states_B_C.shape
+        reqs = rows.state_indices.shape[0]
+        conv = torch.empty(tokens, dim, dtype=rows.hidden_states_B_C.dtype, device=rows.hidden_states_B_C.device)
+        gdn_tree_conv1d_update(
+            rows.hidden_states_B_C.t()[None],
+            rows.conv_state,
+            rows.conv_weight,
+            rows.conv_bias,
+            rows.activation,
+            conv_state_indices=rows.state_indices[:, 0],
+            intermediate_conv_window=None,
+            intermediate_state_indices=None,
+            tree_ancestors=stage.ancestors[: rows.query_start_loc.shape[0] - 1],
+            pad_slot_id=NULL_BLOCK_ID,
+            out=conv.t()[None],
+            num_accepted_tokens=rows.num_accepted_tokens,
+            query_start_loc=rows.query_start_loc,
+        )
+        heads, head_dim, groups, dstate = rows.num_heads, rows.head_dim, rows.n_groups, rows.ssm_state_size
+        x, B, C = conv.split([heads * head_dim, groups * dstate, groups * dstate], dim=-1)
+        mamba2_tree_state_update(
+            rows.ssm_state,
+            x.view(tokens, heads, head_dim),
+            rows.dt,
+            rows.A,
+            B.view(tokens, groups, dstate),
+            C.view(tokens, groups, dstate),
+            rows.D,
+            rows.dt_bias,
+            rows.out.view(tokens, heads, head_dim),
+            state_indices=rows.state_indices,
+            parents=stage.parents,
+            query_start_loc=rows.query_start_loc,
+            num_accepted_tokens=rows.num_accepted_tokens,
+            pad_slot_id=NULL_BLOCK_ID,
+        )
+        published = getattr(stage, "state_slots", {}).get(rows.layer_name)
+        if published is not None:
+            published[:reqs].copy_(rows.state_indices)
 
 
 def _staged() -> Any:

@@ -91,3 +91,69 @@ def test_accepted_counts_pads_and_ragged_requests(dev):
     trees = [_tree("tree", 16, rng), [], _tree("tree", 9, rng)]
     # qsl of an empty request: the tree list holds an empty list; parents / slots rows are padded
     _case(dev, "tp4", trees, seed=9, pads=((0, 3), (2, 0)), accepted=[3, 1, 2])
+
+
+def test_mamba2_layer_front_views(dev):
+    """TreeVerify.forward_mamba2_spec_rows (vllm/gdn_tree_verify.py:107-148): the tree conv over [x | B | C], then
+    the state update on views of the conv output, equals the two kernels run by hand on contiguous copies, bit for
+    bit, and the state update matches the oracle on the conv's own x / B / C."""
+    from types import SimpleNamespace
+
+    from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
+    from eagle_harness.kernels.mamba2_tree import mamba2_tree_state_update
+    from eagle_harness.vllm.gdn_tree_verify import TreeVerify
+    from eagle_harness.vllm.verify_layout import set_stage
+    from oracle.tables import window_codes
+
+    announce("mamba2 layer front views")
+    rng = random.Random(11)
+    heads, head_dim, groups, dstate = 16, 64, 2, 128
+    trees = [_tree("tree", 16, rng) for _ in range(3)]
+    bs, W = len(trees), 16
+    tokens, dim = bs * W, heads * head_dim + 2 * groups * dstate
+    gen = torch.Generator().manual_seed(12)
+    xbc = torch.randn(tokens, dim, generator=gen).bfloat16().to(dev)
+    conv_w = (torch.randn(dim, 4, generator=gen) * 0.3).bfloat16().to(dev)
+    conv_state = torch.zeros(1 + bs * (W + 1), dim, 3 + W, dtype=torch.bfloat16)
+    slots = (1 + torch.arange(bs * (W + 1), dtype=torch.int32)).view(bs, W + 1)
+    conv_state[slots[:, 0].long(), :, :3] = torch.randn(bs, dim, 3, generator=gen).bfloat16()
+    anc = torch.tensor([list(zip(*window_codes(p))) for p in trees], dtype=torch.int32).to(dev)
+    parents = torch.tensor(trees, dtype=torch.int32).to(dev)
+    ssm = (torch.randn(1 + bs * (W + 1), heads, head_dim, dstate, generator=gen) * 0.5).to(dev)
+    dt = torch.randn(tokens, heads, generator=gen).bfloat16().to(dev)
+    A, D, bias = -torch.rand(heads, generator=gen).to(dev), torch.randn(heads).to(dev), torch.randn(heads).to(dev)
+    qsl = torch.arange(0, tokens + 1, W, dtype=torch.int32).to(dev)
+    acc = torch.ones(bs, dtype=torch.int32, device=dev)
+    slots, conv_state = slots.to(dev), conv_state.to(dev)
+
+    rows = SimpleNamespace(hidden_states_B_C=xbc, conv_state=conv_state.clone(), conv_weight=conv_w, conv_bias=None,
+                           activation="silu", state_indices=slots, query_start_loc=qsl, num_accepted_tokens=acc,
+                           num_heads=heads, head_dim=head_dim, n_groups=groups, ssm_state_size=dstate,
+                           ssm_state=ssm.clone(), dt=dt, A=A, D=D, dt_bias=bias, layer_name="layers.1.mixer",
+                           out=torch.zeros(tokens, heads * head_dim, dtype=torch.bfloat16, device=dev))
+    set_stage(SimpleNamespace(ancestors=anc, parents=parents, state_slots={}))
+    try:
+        TreeVerify().forward_mamba2_spec_rows(rows)
+        torch.cuda.synchronize()
+    finally:
+        set_stage(None)
+
+    cs2, ssm2 = conv_state.clone(), ssm.clone()
+    out2 = torch.zeros(tokens, heads, head_dim, dtype=torch.bfloat16, device=dev)
+    conv = torch.empty(tokens, dim, dtype=torch.bfloat16, device=dev)
+    gdn_tree_conv1d_update(xbc.t()[None], cs2, conv_w, None, "silu", slots[:, 0].contiguous(), None, None, anc,
+                           pad_slot_id=0, out=conv.t()[None], num_accepted_tokens=acc, query_start_loc=qsl)
+    x, B, C = (t.contiguous() for t in conv.split([heads * head_dim, groups * dstate, groups * dstate], dim=-1))
+    kw = dict(state_indices=slots, parents=parents, query_start_loc=qsl, num_accepted_tokens=acc, pad_slot_id=0)
+    mamba2_tree_state_update(ssm2, x.view(tokens, heads, head_dim), dt, A, B.view(tokens, groups, dstate),
+                             C.view(tokens, groups, dstate), D, bias, out2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(rows.out.view_as(out2), out2) and torch.equal(rows.ssm_state, ssm2)
+    assert torch.equal(rows.conv_state, cs2)
+    s_want, o_want = ssm.cpu(), torch.zeros(tokens, heads, head_dim, dtype=torch.bfloat16)
+    om.mamba2_tree_state_update(s_want, x.cpu().view(tokens, heads, head_dim), dt.cpu(), A.cpu(),
+                                B.cpu().view(tokens, groups, dstate), C.cpu().view(tokens, groups, dstate), D.cpu(),
+                                bias.cpu(), o_want, **{k: v.cpu() if isinstance(v, torch.Tensor) else v
+                                                       for k, v in kw.items()})
+    torch.testing.assert_close(out2.cpu().float(), o_want.float(), atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(ssm2.cpu(), s_want, atol=1e-5, rtol=1e-4)
