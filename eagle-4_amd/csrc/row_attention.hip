@@ -170,38 +170,33 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
   }
 }
 
-// _merge_splits_kernel (:202-224): one wave per (row, query head); weights 2^(lse - max) over the splits.
+// _merge_splits_kernel (:202-224): D / 4 lanes per (row, query head), 4 consecutive columns each (16-byte loads of
+// the partials), 256 / (D / 4) pairs per workgroup; weights 2^(lse - max) over the splits.
 template <int D, typename T>
-__global__ __launch_bounds__(64) void row_merge_kernel(const eagle4_row_attn_args a, int splits) {
-  constexpr int PL = D / 64 > 0 ? D / 64 : 1;  // elements per lane
-  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
-  const int b = row / a.rows_per_request, t = row % a.rows_per_request;
-  const int64_t part0 = ((static_cast<int64_t>(b) * a.heads + head) * (a.splits + 1)) * a.rows_padded + t;
+__global__ __launch_bounds__(256) void row_merge_kernel(const eagle4_row_attn_args a, int splits) {
+  constexpr int LP = D / 4, PAIRS = 256 / LP;
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * PAIRS + threadIdx.x / LP;
+  const int d = 4 * (threadIdx.x % LP);
+  if (pair >= static_cast<int64_t>(a.bs) * a.rows_per_request * a.heads) return;
+  const int64_t row = pair / a.heads;
+  const int head = static_cast<int>(pair % a.heads);
+  const int64_t b = row / a.rows_per_request, t = row % a.rows_per_request;
+  const int64_t part0 = ((b * a.heads + head) * (a.splits + 1)) * a.rows_padded + t;
   float top = -INFINITY;
   for (int s = 0; s < splits; ++s) top = fmaxf(top, a.part_lse[part0 + s * a.rows_padded]);
-  float wsum = 0.f, accv[PL];
-#pragma unroll
-  for (int e = 0; e < PL; ++e) accv[e] = 0.f;
+  float wsum = 0.f;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < splits; ++s) {
     const int64_t part = part0 + s * a.rows_padded;
     const float lse = a.part_lse[part];
     const float w = lse == -INFINITY ? 0.f : exp2f(lse - top);
     wsum += w;
-    if (w != 0.f) {
-#pragma unroll
-      for (int e = 0; e < PL; ++e) {
-        const int d = lane + 64 * e;
-        if (d < D) accv[e] += w * a.part_out[part * D + d];
-      }
-    }
+    if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t*>(a.part_out + part * D + d);
   }
-  uint16_t* o = static_cast<uint16_t*>(a.out) + static_cast<int64_t>(row) * a.stride_o_row +
-                static_cast<int64_t>(head) * a.stride_o_head;
-#pragma unroll
-  for (int e = 0; e < PL; ++e) {
-    const int d = lane + 64 * e;
-    if (d < D) o[d] = T::from_f32(accv[e] / wsum);
-  }
+  uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.stride_o_row + static_cast<int64_t>(head) * a.stride_o_head + d;
+  const uint32_t lo = T::from_f32(acc.x / wsum) | (static_cast<uint32_t>(T::from_f32(acc.y / wsum)) << 16);
+  const uint32_t hi = T::from_f32(acc.z / wsum) | (static_cast<uint32_t>(T::from_f32(acc.w / wsum)) << 16);
+  *reinterpret_cast<uint2*>(o) = make_uint2(lo, hi);
 }
 
 template <int D, typename T>
@@ -210,7 +205,8 @@ int launch(const eagle4_row_attn_args& a, hipStream_t s) {
   const int groups = (R + 16 * NW - 1) / (16 * NW);
   const int splits = a.splits + (a.step == 0 ? 0 : 1);
   row_attention_kernel<D, T><<<dim3(splits, a.kv_heads * groups, a.bs), NT, 0, s>>>(a, groups);
-  row_merge_kernel<D, T><<<dim3(a.bs * a.rows_per_request, a.heads), 64, 0, s>>>(a, splits);
+  const int64_t pairs = static_cast<int64_t>(a.bs) * a.rows_per_request * a.heads, per = 256 / (D / 4);
+  row_merge_kernel<D, T><<<static_cast<unsigned>((pairs + per - 1) / per), 256, 0, s>>>(a, splits);
   return E4_LAUNCH_STATUS();
 }
 
@@ -236,7 +232,8 @@ extern "C" int eagle4_row_attention(const eagle4_row_attn_args* a, void* stream)
       (a->dtype != EAGLE4_BF16 && a->dtype != EAGLE4_F16) || !al16(a->q) || !al16(a->keys) ||
       (a->values != nullptr && !al16(a->values)) || a->stride_q_row % 8 || a->stride_q_head % 8 ||
       a->k_stride_page % 8 || a->k_stride_slot % 8 || a->k_stride_head % 8 || a->v_stride_page % 8 ||
-      a->v_stride_slot % 8 || a->v_stride_head % 8 ||
+      a->v_stride_slot % 8 || a->v_stride_head % 8 || reinterpret_cast<uintptr_t>(a->out) % 8 ||
+      a->stride_o_row % 4 || a->stride_o_head % 4 ||
       a->part_rows < static_cast<int64_t>(a->bs) * a->heads * (a->splits + 1) * a->rows_padded)
     return EAGLE4_NOT_COVERED;
   const hipStream_t s = static_cast<hipStream_t>(stream);
