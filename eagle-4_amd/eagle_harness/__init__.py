@@ -4,7 +4,9 @@ This ``eagle_harness`` holds only the verify path of eagle-harness 0.1.5, with t
 callers drop in unchanged:
 
 - ``eagle_harness.kernels``: ``gdn_tree`` (tree tables), ``gdn_tree_conv``, ``gdn_tree_recurrence``,
-  ``gdn_tree_records``, ``accept_tail``, ``verify_prep``, ``online_softmax``, ``arch``;
+  ``gdn_tree_records``, ``accept_tail``, ``verify_prep``, ``row_attention``, ``mamba2_tree``, ``arch``
+  (the reference's ``online_softmax`` is a Triton helper inlined into its attention kernels; its step lives inside
+  the HIP attention kernels here, so there is no module for it);
 - ``eagle_harness.vllm``: ``verify_attention``, ``verify_layout`` (the verify stage), ``tree_accept`` (the walk) and
   ``gdn_tree_verify`` (the accepted-path state commit), all engine-free.
 

@@ -10,7 +10,8 @@ module              what
 ``gdn_tree_records``     replay records and the accepted-path commit (records contract)
 ``accept_tail``     bs1 greedy accept tail and row compaction
 ``verify_prep``     tail-mask words
-``online_softmax``  where the online-softmax step lives (inside the HIP attention kernel)
+``row_attention``   draft-side row attention (sliding window + tree ancestors)
+``mamba2_tree``     Mamba2 tree selective state update
 ==================  =====================================================================================
 
 The kernels are compiled ahead of time into ``libeagle4_amd.so`` (``python eagle-4_amd/build.py``); ``_native`` binds

@@ -18,15 +18,16 @@ LANES = 32
 
 
 class Accepted(NamedTuple):
-    """What a greedy tree verify of one request accepted (kernels/accept_tail.py:37-46)."""
+    """Result of :func:`accept_tail` for one request (the fields of kernels/accept_tail.py:37-46). ``W`` is the
+    tree width, ``depth`` the caller's maximum number of accepted tokens; ``n`` below is ``accept_lens[0]``."""
 
-    predict: torch.Tensor  # int32 [width]: target token of each accepted node, the accepted path moved to the front
-    accept_index: torch.Tensor  # int32 [1, depth]: node of each accepted token, -1 padded
-    accept_lens: torch.Tensor  # int32 [1]: accepted drafts + the bonus token
-    new_seq_lens: torch.Tensor  # [1], seq_lens + accept_lens
-    bonus_tokens: torch.Tensor  # int32 [1]: the last accepted token
-    committed_slots: torch.Tensor  # int64 [depth]: KV slots the accepted tokens move to (0 past accept_lens)
-    accepted_slots: torch.Tensor  # int64 [depth]: KV slots they were written to by the verify (0 past accept_lens)
+    predict: torch.Tensor  # [W] int32; entries 0..n-1: the target's token at each accepted node, root first
+    accept_index: torch.Tensor  # [1, depth] int32; the accepted nodes' rows, then -1
+    accept_lens: torch.Tensor  # [1] int32; n = accepted draft tokens + 1 (the target's own token at the end)
+    new_seq_lens: torch.Tensor  # [1], dtype of seq_lens; seq_lens + n
+    bonus_tokens: torch.Tensor  # [1] int32; predict[n - 1]
+    committed_slots: torch.Tensor  # [depth] int64; KV slot where accepted token i belongs after the round, then 0
+    accepted_slots: torch.Tensor  # [depth] int64; KV slot the verify forward wrote accepted token i to, then 0
 
 
 def accept_tail(
@@ -82,9 +83,10 @@ def accept_tail(
 def compact_rows(
     rows: torch.Tensor, accept_index: torch.Tensor, block: int = 2048, out: Optional[torch.Tensor] = None
 ) -> torch.Tensor:
-    """A copy of the node-indexed ``rows`` [width, cols] whose first ``accept_index.shape[1]`` rows are the accepted
-    path (padding: row 0), the other rows unchanged; into ``out`` (same shape, not ``rows``) if given
-    (kernels/accept_tail.py:209-224). ``block`` is accepted for signature compatibility."""
+    """Gathers the accepted rows of ``rows`` [W, cols] (indexed by tree node) to the front: row ``i`` of the result
+    is ``rows[accept_index[0, i]]`` for ``i < accept_index.shape[1]`` (an index of -1 reads node 0) and ``rows[i]``
+    after that (kernels/accept_tail.py:209-224). The result goes to ``out`` when given (``rows``' shape, unit column
+    stride, another buffer), else to a new tensor. ``block`` only keeps the reference's signature."""
     width, cols = rows.shape
     if rows.stride(1) != 1:
         raise ValueError("compact_rows needs rows with a unit column stride")
@@ -108,21 +110,13 @@ def compact_rows(
 
 
 def warm_up(hidden_rows: torch.Tensor, hidden_dtype: torch.dtype) -> None:
-    """Runs :func:`accept_tail` and :func:`compact_rows` once before serving (kernels/accept_tail.py:227-249). The
-    kernels are compiled ahead of time, so this only exercises the launch path; its first two rows are overwritten."""
-    long = dict(dtype=torch.int64, device=hidden_rows.device)
-    tokens = torch.zeros(2, **long)
-    tables = torch.tensor([[1, -1]], **long)
-    accepted = accept_tail(
-        tokens,
-        tokens,
-        torch.arange(2, **long).reshape(1, 2),
-        tables,
-        tables,
-        torch.ones(1, **long),
-        tokens,
-        torch.zeros(1, 4, dtype=torch.int32, device=hidden_rows.device),
-        torch.zeros(1, **long),
-        2,
-    )
-    compact_rows(torch.zeros_like(hidden_rows[:2], dtype=hidden_dtype), accepted.accept_index, out=hidden_rows[:2])
+    """Launch check before serving (kernels/accept_tail.py:227-249). The reference compiles its two kernels here;
+    these are compiled ahead of time, so one launch of each on ``hidden_rows``' device is what is left to do: it
+    loads the library there and surfaces a launch failure before the first request. The tree is a lone root (always
+    accepted); row 0 of ``hidden_rows`` receives zeros of ``hidden_dtype``, the dtype the served compaction copies."""
+    device = hidden_rows.device
+    one = lambda value: torch.full((1, 1), value, dtype=torch.int64, device=device)  # noqa: E731
+    got = accept_tail(one(0), one(0), one(0), one(-1), one(-1), one(1), one(0),
+                      torch.zeros(1, 2, dtype=torch.int32, device=device), one(0), 1)
+    compact_rows(torch.zeros(1, hidden_rows.shape[1], dtype=hidden_dtype, device=device), got.accept_index,
+                 out=hidden_rows[:1])

@@ -1,17 +1,21 @@
-"""Which GPU can run which kernel: the single place that reads a device's architecture (kernels/arch.py).
+"""Device gate of the gfx950 library: which visible GPU the kernels run on, and the launch features callers ask about.
 
-The kernels here are built for one target, gfx950 (MI355X). Importing this module never initialises the GPU and never
-raises; :func:`unsupported_reason` says why a device is not covered and :func:`require_supported` raises
-:class:`UnsupportedHardware` with that message. The feature predicates keep the reference's names (kernels/arch.py:
-122-171) so callers read them unchanged: PDL, clusters and the Gluon GDN twin are NVIDIA features and are off; the
-records-replay commit is on (the AMD default of the reference).
+``libeagle4_amd.so`` carries code objects for a single ISA, gfx950 (MI355X, CDNA4). A device is covered exactly when
+the ISA part of its target name (``gcnArchName`` up to the first ``:``, e.g. ``gfx950`` of
+``gfx950:sramecc+:xnack-``) is that ISA; nothing else about the device changes which kernel runs. Looking a device
+up goes through torch's device properties only, so importing this module does not touch the GPU, and asking about a
+machine without one returns a reason instead of raising.
+
+The feature predicates are the names the reference's launchers call (kernels/arch.py:122-171). Each is a fixed answer
+for a covered gfx950 device, listed in :data:`FEATURES` with the reason, and False for any device that is not
+covered.
 """
 
 from __future__ import annotations
 
 import functools
 from dataclasses import dataclass
-from typing import Optional, Union
+from typing import Callable, Optional, Union
 
 import torch
 
@@ -22,115 +26,123 @@ DeviceLike = Union[None, int, str, torch.device]
 
 
 class UnsupportedHardware(RuntimeError):
-    """The visible GPU (or the software stack) is outside what the kernels cover."""
+    """Raised by :func:`require_supported` when the device cannot run the gfx950 code objects."""
 
 
 @dataclass(frozen=True)
 class Gpu:
-    """One visible GPU: index, name, vendor and architecture."""
+    """What the gate knows about one visible device."""
 
     index: int
     name: str
-    vendor: str
-    arch: str
-    sm: int = 0
+    vendor: str  # "amd" on a ROCm build of torch, "nvidia" on a CUDA build
+    arch: str  # ISA name: "gfx950"; "sm_90" style on NVIDIA
+    sm: int = 0  # NVIDIA compute capability (major * 10 + minor); 0 on AMD
+    target: str = ""  # the full target string with its feature flags, e.g. "gfx950:sramecc+:xnack-"
+    compute_units: int = 0
 
     @property
     def nvidia(self) -> bool:
         return self.vendor == "nvidia"
 
 
-def _index(device: DeviceLike) -> Optional[int]:
+def _device_index(device: DeviceLike) -> Optional[int]:
+    """Index of a GPU device spec; None for anything that names a non-GPU device."""
+    if device is None:
+        return torch.cuda.current_device()
     if isinstance(device, int):
         return device
-    dev = torch.device("cuda" if device is None else device)
-    if dev.type != "cuda":
+    spec = torch.device(device)
+    if spec.type != "cuda":
         return None
-    return torch.cuda.current_device() if dev.index is None else dev.index
+    return spec.index if spec.index is not None else torch.cuda.current_device()
 
 
 @functools.lru_cache(maxsize=None)
-def _probe(index: int) -> Gpu:
+def _describe(index: int) -> Gpu:
     props = torch.cuda.get_device_properties(index)
-    if torch.version.hip:
-        return Gpu(index, props.name, "amd", props.gcnArchName.split(":")[0], 0)
-    return Gpu(index, props.name, "nvidia", f"sm_{props.major}{props.minor}", props.major * 10 + props.minor)
+    cus = int(getattr(props, "multi_processor_count", 0))
+    if torch.version.hip is None:
+        cc = props.major * 10 + props.minor
+        return Gpu(index, props.name, "nvidia", f"sm_{cc}", cc, "", cus)
+    target = str(props.gcnArchName)
+    return Gpu(index, props.name, "amd", target.partition(":")[0], 0, target, cus)
 
 
 def gpu(device: DeviceLike = None) -> Optional[Gpu]:
-    """The GPU behind ``device`` (default: the current one), None without one."""
+    """Description of the device behind ``device`` (the current one by default); None when there is no GPU."""
     if not torch.cuda.is_available():
         return None
-    index = _index(device)
-    return _probe(index) if index is not None else None
+    index = _device_index(device)
+    return None if index is None else _describe(index)
 
 
 def unsupported_reason(device: DeviceLike = None) -> Optional[str]:
-    """None when the kernels run on ``device``, else a one-line reason."""
-    g = gpu(device)
-    if g is None:
-        return "no ROCm device is visible to torch"
-    if g.nvidia or g.arch not in AMD_ARCHS:
-        return f"{g.name} ({g.arch}) is not {TARGET_ARCH} (MI355X); the kernels are built for {TARGET_ARCH} only"
+    """Why the kernels cannot run on ``device``, in one line; None when they can."""
+    found = gpu(device)
+    if found is None:
+        return "torch sees no ROCm GPU"
+    if found.arch != TARGET_ARCH:
+        return (f"{found.name} is {found.arch or 'an unknown ISA'}, and libeagle4_amd.so holds {TARGET_ARCH} "
+                f"(MI355X) code objects only")
     return None
 
 
 def require_supported(device: DeviceLike = None) -> Gpu:
-    """The GPU behind ``device``; raises :class:`UnsupportedHardware` where the kernels do not run."""
-    if (reason := unsupported_reason(device)) is not None:
-        raise UnsupportedHardware(f"eagle4_amd kernels are off: {reason}.")
+    """The covered device behind ``device``; :class:`UnsupportedHardware` otherwise."""
+    reason = unsupported_reason(device)
+    if reason is not None:
+        raise UnsupportedHardware(f"eagle4_amd: the gfx950 kernels cannot run here: {reason}")
     return gpu(device)  # type: ignore[return-value]
 
 
-def _ours(device: DeviceLike) -> bool:
-    return unsupported_reason(device) is None
+# Launch features, as the reference's launchers name them: the answer on a covered gfx950 device, and why.
+FEATURES: dict[str, tuple[bool, str]] = {
+    "native_candidate_tail": (False, "the candidate tail is a CUDA kernel; its HIP counterpart is not on this path"),
+    "clusters": (False, "thread-block clusters are a CUDA launch attribute; CDNA4 has no counterpart"),
+    "pdl": (False, "programmatic dependent launch is CUDA-only; these kernels follow plain stream order"),
+    "gluon_gdn": (False, "the Gluon GDN walk targets NVIDIA sm_103; the HIP walk serves every shape here"),
+    "draftmk": (False, "the draft-round megakernel ships as sm_103a code only"),
+    "gdn_records_replay": (True, "GDN verify keeps replay records and commits the accepted path, the AMD default"),
+    "side_stream_prelaunch": (False, "the next round's draft work stays on the caller's stream on AMD"),
+}
 
 
-def native_candidate_tail(device: DeviceLike = None) -> bool:
-    """The CUDA candidate-tail kernel: NVIDIA only."""
-    return False
+def _feature(name: str) -> Callable[[DeviceLike], bool]:
+    on, why = FEATURES[name]
+
+    def predicate(device: DeviceLike = None) -> bool:
+        return on and unsupported_reason(device) is None
+
+    predicate.__name__ = predicate.__qualname__ = name
+    predicate.__doc__ = f"{'On' if on else 'Off'} for gfx950: {why}."
+    return predicate
 
 
-def clusters(device: DeviceLike = None) -> bool:
-    """Thread-block clusters: NVIDIA only."""
-    return False
-
-
-def pdl(device: DeviceLike = None) -> bool:
-    """Programmatic dependent launch: NVIDIA only; the HIP kernels here run in stream order."""
-    return False
-
-
-def gluon_gdn(device: DeviceLike = None) -> bool:
-    """The Gluon GDN twin: NVIDIA sm_103 only."""
-    return False
-
-
-def draftmk(device: DeviceLike = None) -> bool:
-    """The draft-round megakernel: NVIDIA B300 only."""
-    return False
-
-
-def gdn_records_replay(device: DeviceLike = None) -> bool:
-    """Replay records plus an accepted-path commit instead of per-node snapshots (the reference's AMD default)."""
-    return _ours(device)
-
-
-def side_stream_prelaunch(device: DeviceLike = None) -> bool:
-    """Draft prelaunch on a side stream: off on AMD, as in the reference."""
-    return False
+native_candidate_tail = _feature("native_candidate_tail")
+clusters = _feature("clusters")
+pdl = _feature("pdl")
+gluon_gdn = _feature("gluon_gdn")
+draftmk = _feature("draftmk")
+gdn_records_replay = _feature("gdn_records_replay")
+side_stream_prelaunch = _feature("side_stream_prelaunch")
 
 
 def report() -> str:
-    """One line per visible device."""
+    """Every visible device with its verdict, and the feature answers when it is covered."""
     if not torch.cuda.is_available():
-        return f"no GPU visible: {unsupported_reason()}"
-    lines = []
-    for i in range(torch.cuda.device_count()):
-        g = _probe(i)
-        reason = unsupported_reason(i)
-        lines.append(f"cuda:{i} {g.name} ({g.arch}): " + (f"OFF, {reason}" if reason else "supported"))
-    return "\n".join(lines)
+        return f"no device: {unsupported_reason()}"
+    out = []
+    for index in range(torch.cuda.device_count()):
+        found = _describe(index)
+        reason = unsupported_reason(index)
+        head = f"cuda:{index} {found.name} [{found.target or found.arch}, {found.compute_units} CUs]"
+        if reason is not None:
+            out.append(f"{head}: not covered ({reason})")
+            continue
+        flags = " ".join(f"{name}={'on' if on else 'off'}" for name, (on, _) in FEATURES.items())
+        out.append(f"{head}: covered; {flags}")
+    return "\n".join(out)
 
 
 if __name__ == "__main__":

@@ -36,31 +36,41 @@ def gdn_tree_state_args(
     intermediate_state_indices: torch.Tensor,
     publish: Optional[torch.Tensor],
 ) -> dict:
-    """The state-addressing arguments of a walk launch, after checking the layout
-    (kernels/gdn_tree_recurrence.py:517-559; same assertions and keys)."""
-    row_slots = intermediate_state_indices.ndim == 2
-    if row_slots:
-        assert intermediate_states_buffer.ndim == 4, "one slot per row addresses a [slots, HV, V, K] buffer"
+    """Checks how a walk launch addresses its states and returns the addressing values keyed by the reference walk's
+    argument names (kernels/gdn_tree_recurrence.py:517-559; the keys and the assertion messages are the interface
+    the reference's callers read).
+
+    A per-row slot table ([N, S] into a [slots, HV, V, K] pool, vLLM) or a per-request table ([N] into a
+    [slots, steps, HV, V, K] scratch, sglang) selects the layout; ``num_accepted_tokens`` comes with, and only with,
+    a 2-D initial-state table; ``publish`` needs per-row slots. Entries the chosen layout does not read hold a
+    stride of 0, or a tensor that is safe to pass, and the flags say so."""
+    per_row = intermediate_state_indices.dim() == 2
+    if per_row:
+        assert intermediate_states_buffer.dim() == 4, "one slot per row addresses a [slots, HV, V, K] buffer"
     else:
-        assert intermediate_states_buffer.ndim == 5, "one slot per request addresses a [slots, steps, HV, V, K] buffer"
-    assert (initial_state_indices.ndim == 2) == (num_accepted_tokens is not None)
-    assert publish is None or row_slots, "publish copies a table of per-row slots"
-    return dict(
-        stride_h0_source=initial_state_source.stride(0),
-        stride_h0_indices_seq=initial_state_indices.stride(0),
-        stride_h0_indices_col=initial_state_indices.stride(1) if initial_state_indices.ndim == 2 else 0,
-        num_accepted=initial_state_indices if num_accepted_tokens is None else num_accepted_tokens,
-        stride_snap_indices_seq=intermediate_state_indices.stride(0),
-        stride_snap_indices_row=intermediate_state_indices.stride(1) if row_slots else 0,
-        stride_snap_slot=intermediate_states_buffer.stride(0),
-        stride_snap_row=0 if row_slots else intermediate_states_buffer.stride(1),
-        publish=intermediate_state_indices if publish is None else publish,
-        stride_publish=0 if publish is None else publish.stride(0),
-        num_slot_cols=intermediate_state_indices.shape[-1],
-        ROW_SLOTS=row_slots,
-        HAS_NUM_ACCEPTED=num_accepted_tokens is not None,
-        PUBLISH=publish is not None,
-    )
+        assert intermediate_states_buffer.dim() == 5, "one slot per request addresses a [slots, steps, HV, V, K] buffer"
+    h0_per_column = initial_state_indices.dim() == 2
+    assert h0_per_column == (num_accepted_tokens is not None)
+    assert publish is None or per_row, "publish copies a table of per-row slots"
+
+    def inner_stride(t: torch.Tensor) -> int:  # column stride of a 2-D table; 0 for a 1-D one
+        return t.stride(1) if t.dim() == 2 else 0
+
+    found = {
+        "stride_h0_source": initial_state_source.stride(0),
+        "stride_h0_indices_seq": initial_state_indices.stride(0),
+        "stride_h0_indices_col": inner_stride(initial_state_indices),
+        "num_accepted": num_accepted_tokens if h0_per_column else initial_state_indices,
+        "stride_snap_indices_seq": intermediate_state_indices.stride(0),
+        "stride_snap_indices_row": inner_stride(intermediate_state_indices),
+        "stride_snap_slot": intermediate_states_buffer.stride(0),
+        "stride_snap_row": 0 if per_row else intermediate_states_buffer.stride(1),
+        "publish": publish if publish is not None else intermediate_state_indices,
+        "stride_publish": publish.stride(0) if publish is not None else 0,
+        "num_slot_cols": intermediate_state_indices.shape[-1],
+    }
+    found.update(ROW_SLOTS=per_row, HAS_NUM_ACCEPTED=h0_per_column, PUBLISH=publish is not None)
+    return found
 
 
 def _check_state_layout(t: torch.Tensor, lead: int, HV: int, V: int, K: int, name: str) -> None:

@@ -128,48 +128,50 @@ class TreeVerify:
     def __init__(self, vllm_config: Any = None):
         self.vllm_config = vllm_config
 
+    @staticmethod
+    def _tree_conv(stage: Any, rows: Any, packed: torch.Tensor) -> torch.Tensor:
+        """The width-4 tree conv of a layer's packed input ``packed`` [tokens, channels] (a token-strided view of the
+        input projection is read in place) into a new [tokens, channels] tensor. Each request's history is the conv
+        state of its slot column 0, read from column ``num_accepted - 1``; the stage's window codes name each row's
+        three ancestors."""
+        result = torch.empty(packed.shape, dtype=packed.dtype, device=packed.device)
+        num_reqs = rows.query_start_loc.shape[0] - 1
+        gdn_tree_conv1d_update(packed.t()[None], rows.conv_state, rows.conv_weight, rows.conv_bias, rows.activation,
+                               conv_state_indices=rows.state_indices[:, 0], intermediate_conv_window=None,
+                               intermediate_state_indices=None, tree_ancestors=stage.ancestors[:num_reqs],
+                               pad_slot_id=NULL_BLOCK_ID, out=result.t()[None],
+                               num_accepted_tokens=rows.num_accepted_tokens, query_start_loc=rows.query_start_loc)
+        return result
+
+    @staticmethod
+    def _column_views(mixed: torch.Tensor, widths: Sequence[int]) -> list[torch.Tensor]:
+        """Consecutive column blocks of ``mixed`` [tokens, sum(widths)] as views (no copies)."""
+        views, col = [], 0
+        for w in widths:
+            views.append(mixed[:, col : col + w])
+            col += w
+        return views
+
     def forward_spec_rows(self, rows: GDNSpecRows) -> None:
+        """Conv, then the gated delta rule walk over the stage's trees; the walk's snapshots go to the per-row
+        slots ``rows.state_indices`` of ``rows.ssm_state`` and its output to ``rows.out``."""
         stage = _staged()
-        tokens, dim = rows.mixed_qkv.shape
-        conv = torch.empty(tokens, dim, dtype=rows.mixed_qkv.dtype, device=rows.mixed_qkv.device)
-        gdn_tree_conv1d_update(
-            rows.mixed_qkv.t()[None],
-            rows.conv_state,
-            rows.conv_weight,
-            rows.conv_bias,
-            rows.activation,
-            conv_state_indices=rows.state_indices[:, 0],
-            intermediate_conv_window=None,
-            intermediate_state_indices=None,
-            tree_ancestors=stage.ancestors[: rows.query_start_loc.shape[0] - 1],
-            pad_slot_id=NULL_BLOCK_ID,
-            out=conv.t()[None],
-            num_accepted_tokens=rows.num_accepted_tokens,
-            query_start_loc=rows.query_start_loc,
-        )
-        key_dim = rows.num_k_heads * rows.head_k_dim
-        q, k, v = conv.split([key_dim, key_dim, rows.num_v_heads * rows.head_v_dim], dim=-1)
-        published = getattr(stage, "state_slots", {}).get(rows.layer_name)
+        mixed = self._tree_conv(stage, rows, rows.mixed_qkv)
+        tokens = mixed.shape[0]
+        kdim, vdim = rows.num_k_heads * rows.head_k_dim, rows.num_v_heads * rows.head_v_dim
+        q, k, v = self._column_views(mixed, (kdim, kdim, vdim))
+        per_head = lambda t, d: t.view(1, tokens, -1, d)  # noqa: E731  [1, tokens, heads, d], token-strided
+        slot_rows = rows.state_indices
+        publish = stage.state_slots.get(rows.layer_name)  # set for the one layer per KV cache group that publishes
         gdn_tree_recurrent_update(
-            rows.A_log,
-            rows.dt_bias,
-            q.view(1, tokens, -1, rows.head_k_dim),
-            k.view(1, tokens, -1, rows.head_k_dim),
-            v.view(1, tokens, -1, rows.head_v_dim),
-            rows.a,
-            rows.b,
-            initial_state_source=rows.ssm_state,
-            initial_state_indices=rows.state_indices,
-            num_accepted_tokens=rows.num_accepted_tokens,
-            cu_seqlens=rows.query_start_loc,
-            intermediate_states_buffer=rows.ssm_state,
-            intermediate_state_indices=rows.state_indices,
-            retrieve_parent_token=stage.parents,
-            pad_slot_id=NULL_BLOCK_ID,
-            out=rows.out.view(1, tokens, -1, rows.head_v_dim),
-            publish=None if published is None else published[: rows.state_indices.shape[0]],
-            gluon=True,
-        )
+            rows.A_log, rows.dt_bias, per_head(q, rows.head_k_dim), per_head(k, rows.head_k_dim),
+            per_head(v, rows.head_v_dim), rows.a, rows.b,
+            initial_state_source=rows.ssm_state, initial_state_indices=slot_rows,
+            num_accepted_tokens=rows.num_accepted_tokens, cu_seqlens=rows.query_start_loc,
+            intermediate_states_buffer=rows.ssm_state, intermediate_state_indices=slot_rows,
+            retrieve_parent_token=stage.parents, pad_slot_id=NULL_BLOCK_ID,
+            out=per_head(rows.out, rows.head_v_dim),
+            publish=None if publish is None else publish[: slot_rows.shape[0]], gluon=True)
 
     def forward_mamba2_spec_rows(self, rows: Any) -> None:
         """A Mamba2 layer's decode rows (vllm/gdn_tree_verify.py:107-148): the tree conv over ``hidden_states_B_C``,
@@ -178,45 +180,20 @@ class TreeVerify:
         query_start_loc, num_accepted_tokens, num_heads, head_dim, n_groups, ssm_state_size, ssm_state, dt, A, D,
         dt_bias, out, layer_name)."""
         stage = _staged()
-        tokens, dim = rows.hidden_states_B_C.shape
-        reqs = rows.state_indices.shape[0]
-        conv = torch.empty(tokens, dim, dtype=rows.hidden_states_B_C.dtype, device=rows.hidden_states_B_C.device)
-        gdn_tree_conv1d_update(
-            rows.hidden_states_B_C.t()[None],
-            rows.conv_state,
-            rows.conv_weight,
-            rows.conv_bias,
-            rows.activation,
-            conv_state_indices=rows.state_indices[:, 0],
-            intermediate_conv_window=None,
-            intermediate_state_indices=None,
-            tree_ancestors=stage.ancestors[: rows.query_start_loc.shape[0] - 1],
-            pad_slot_id=NULL_BLOCK_ID,
-            out=conv.t()[None],
-            num_accepted_tokens=rows.num_accepted_tokens,
-            query_start_loc=rows.query_start_loc,
-        )
-        heads, head_dim, groups, dstate = rows.num_heads, rows.head_dim, rows.n_groups, rows.ssm_state_size
-        x, B, C = conv.split([heads * head_dim, groups * dstate, groups * dstate], dim=-1)
+        mixed = self._tree_conv(stage, rows, rows.hidden_states_B_C)
+        tokens = mixed.shape[0]
+        group_cols = rows.n_groups * rows.ssm_state_size
+        x, B, C = self._column_views(mixed, (rows.num_heads * rows.head_dim, group_cols, group_cols))
+        slot_rows = rows.state_indices
         mamba2_tree_state_update(
-            rows.ssm_state,
-            x.view(tokens, heads, head_dim),
-            rows.dt,
-            rows.A,
-            B.view(tokens, groups, dstate),
-            C.view(tokens, groups, dstate),
-            rows.D,
-            rows.dt_bias,
-            rows.out.view(tokens, heads, head_dim),
-            state_indices=rows.state_indices,
-            parents=stage.parents,
-            query_start_loc=rows.query_start_loc,
-            num_accepted_tokens=rows.num_accepted_tokens,
-            pad_slot_id=NULL_BLOCK_ID,
-        )
-        published = getattr(stage, "state_slots", {}).get(rows.layer_name)
-        if published is not None:
-            published[:reqs].copy_(rows.state_indices)
+            rows.ssm_state, x.view(tokens, rows.num_heads, rows.head_dim), rows.dt, rows.A,
+            B.view(tokens, rows.n_groups, rows.ssm_state_size), C.view(tokens, rows.n_groups, rows.ssm_state_size),
+            rows.D, rows.dt_bias, rows.out.view(tokens, rows.num_heads, rows.head_dim), state_indices=slot_rows,
+            parents=stage.parents, query_start_loc=rows.query_start_loc, num_accepted_tokens=rows.num_accepted_tokens,
+            pad_slot_id=NULL_BLOCK_ID)
+        publish = stage.state_slots.get(rows.layer_name)
+        if publish is not None:  # the Mamba2 update has no publish argument: copy the slot rows in stream order
+            publish[: slot_rows.shape[0]].copy_(slot_rows)
 
 
 def _staged() -> Any:

@@ -33,22 +33,32 @@ class KvCompactor:
         table_block_sizes: Sequence[int],
         device: torch.device,
     ):
-        first = kv_caches[0]
-        view = first.transpose(1, 2)  # (blocks, slots in a block, heads, 2 * head_dim)
-        if any(c.transpose(1, 2).stride() != view.stride() or c.dtype != first.dtype for c in kv_caches):
-            raise ValueError("the target's full-attention layers must share one KV cache layout")
-        if view.stride(3) != 1:
+        # The backend's cache is (blocks, heads, slots in a block, 2 * head_dim), a token's K and V adjacent; the
+        # kernel walks (block, slot, head), so validate on that order. The checks and messages are the reference's
+        # (vllm/round_commit.py:93-116), which callers may rely on.
+        views = [cache.transpose(1, 2) for cache in kv_caches]
+        ref = views[0]
+        for cache, v in zip(kv_caches, views):
+            if v.stride() != ref.stride() or cache.dtype != kv_caches[0].dtype:
+                raise ValueError("the target's full-attention layers must share one KV cache layout")
+        if ref.stride(3) != 1:
             raise ValueError("KV cache rows must be contiguous")
-        self.strides = (view.stride(0), view.stride(2), view.stride(1))  # block, head, slot
-        self.num_heads, self.dim, self.dtype = view.shape[2], view.shape[3], first.dtype
-        self.block_size = view.shape[1]
+        for table in block_tables:
+            if table.dtype != torch.int32:
+                raise ValueError("block tables must be int32")
+        stride_block, stride_slot, stride_head = ref.stride(0), ref.stride(1), ref.stride(2)
+        self.strides = (stride_block, stride_head, stride_slot)
+        self.block_size, self.num_heads, self.dim = ref.shape[1], ref.shape[2], ref.shape[3]
+        self.dtype = kv_caches[0].dtype
         self.device = device
-        self.layer_ptrs = torch.tensor([c.data_ptr() for c in kv_caches], dtype=torch.uint64, device=device)
-        self.table_ptrs = torch.tensor([t.data_ptr() for t in block_tables], dtype=torch.uint64, device=device)
-        self.table_strides = torch.tensor([t.stride(0) for t in block_tables], dtype=torch.int64, device=device)
-        self.table_block_sizes = torch.tensor(list(table_block_sizes), dtype=torch.int32, device=device)
-        if any(t.dtype != torch.int32 for t in block_tables):
-            raise ValueError("block tables must be int32")
+
+        def on_device(values, dtype):
+            return torch.tensor(list(values), dtype=dtype, device=device)
+
+        self.layer_ptrs = on_device((c.data_ptr() for c in kv_caches), torch.uint64)
+        self.table_ptrs = on_device((t.data_ptr() for t in block_tables), torch.uint64)
+        self.table_strides = on_device((t.stride(0) for t in block_tables), torch.int64)
+        self.table_block_sizes = on_device(table_block_sizes, torch.int32)
         self._keep = (list(kv_caches), list(block_tables))
 
     def compact(

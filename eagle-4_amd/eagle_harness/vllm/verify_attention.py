@@ -1,13 +1,22 @@
-"""Attention of a tree verify forward's full-attention layers, split over the committed context
-(vllm/verify_attention.py).
+"""Tree-verify attention of a verify forward's full-attention layers (vllm/verify_attention.py), engine-free.
 
 A request's ``W`` verify rows attend to its committed context in the paged KV cache (the same keys for every row)
-and to their own tree ancestors among the ``W`` new tokens. The gfx950 kernel (``csrc/verify_attention.hip``) runs
-one workgroup per (context split, KV head, request) whose waves own the ``G x W`` query rows of the KV head (``G``
-query heads per KV head), so each K / V tile is read from HBM once for all of them; a second kernel merges the splits
-by their log-sum-exp. The cache may be bf16 / fp16, or fp8-e4m3 (OCP) with one fp32 scale per (page, KV head) for
-keys (``k_scale``) and values (``v_scale``), dequantised inside the tile loads: new function relative to the
-reference, whose vLLM backend refuses quantized caches (vllm/tree_attention.py:69-70).
+and to their own tree ancestors among the ``W`` new tokens. Every kernel reads each K / V tile once for all ``G x W``
+rows of a KV head (``G`` query heads per KV head); the reference's grid is per query head and reads it ``G`` times.
+Three schedules (``csrc/``):
+
+- ``verify_attention_stream.hip`` (default for 16-bit and fp8 pages, up to 1024 requests): a persistent grid of one
+  workgroup per resident slot takes equal contiguous shares of all (request, KV head, row group) tiles of 32 keys
+  (64 fp8 keys), streamed into LDS by producer waves; segments cut by a share boundary leave fp32 partials that a
+  second kernel merges by their log-sum-exp.
+- ``verify_attention.hip`` (more requests, or a caller-chosen ``chunk``): one workgroup per (context split, KV head,
+  request), then the same merge.
+- ``verify_attention_f32.hip``: fp32 rows over fp32 pages (the reference test's dtype).
+
+The cache may be bf16 / fp16, or fp8-e4m3 (OCP) with one fp32 scale per (page, KV head) for keys (``k_scale``) and
+values (``v_scale``), dequantised inside the kernels: new function relative to the reference, whose vLLM backend
+refuses quantized caches (vllm/tree_attention.py:69-70); :mod:`eagle_harness.vllm.tree_attention` routes such caches
+here.
 """
 
 from __future__ import annotations
@@ -17,9 +26,6 @@ from typing import Optional
 import torch
 
 from eagle_harness.kernels import _native
-
-BLOCK = 64  # context keys per inner step (the kernel's KV tile)
-
 
 def verify_attention(
     q: torch.Tensor,
@@ -47,7 +53,8 @@ def verify_attention(
     first ``context_lens[b]`` tokens through ``block_table[b]``; ``masks[b, r]`` has bit ``j`` set iff new token
     ``j`` is row ``r`` or one of its ancestors. Every request has at most ``max_query_len`` (<= 64) rows.
     ``k_scale`` / ``v_scale``: fp32 ``[blocks, Hkv]`` scales of an fp8-e4m3 cache. ``chunk``: context keys per split
-    (a multiple of 64; 0 lets the library choose).
+    of the split-context schedule (a multiple of 64; 0 lets the library choose the streamed schedule where it
+    applies).
     """
     num_reqs = query_start_loc.shape[0] - 1
     heads, head_dim = q.shape[1], q.shape[2]
@@ -56,6 +63,14 @@ def verify_attention(
         raise ValueError("an fp8-e4m3 cache needs k_scale and v_scale ([blocks, Hkv] fp32)")
     if fp8 and (k_scale.dtype != torch.float32 or v_scale.dtype != torch.float32):
         raise ValueError("k_scale / v_scale must be fp32")
+    if value_cache.dtype != key_cache.dtype:
+        raise _native.NotCovered(f"key_cache is {key_cache.dtype} but value_cache is {value_cache.dtype}")
+    if fp8:
+        blocks, kv_heads = key_cache.shape[0], key_cache.shape[2]
+        for name, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+            if sc.dim() != 2 or sc.shape[0] < blocks or sc.shape[1] < kv_heads or sc.device != key_cache.device:
+                raise ValueError(f"{name} must be [blocks >= {blocks}, Hkv >= {kv_heads}] fp32 on the cache's device, "
+                                 f"got {tuple(sc.shape)}")
     if block_table.dtype != torch.int32:
         raise _native.NotCovered("the block table must be int32")
     for name, t in (("q", q), ("k_new", k_new), ("v_new", v_new), ("out", out), ("key_cache", key_cache),

@@ -1,10 +1,13 @@
-"""The tree of the current verify forward, in buffers that graphs replay (vllm/verify_layout.py).
+"""Verify-round tree tables kept in fixed buffers, so a captured HIP graph sees the current round's trees
+(the role of vllm/verify_layout.py).
 
-``propose`` stores the parent row of every verify row of a request (:class:`TreeStore`, by request state slot).
-Before each target forward :meth:`VerifyStage.stage` gathers the batch's rows into :class:`VerifyStage` (by batch
-row) and rewrites the forward's positions from chain positions to depths, in one gfx950 launch
-(``csrc/tree_tables.hip``). Row 0 of a request is the root; rows are parent first, so any prefix of the rows is a
-tree too.
+Two holders. :class:`TreeStore` is indexed by request state slot and outlives a round: the drafter writes each
+request's parent rows into it, the accept walk writes the accepted rows back. :class:`VerifyStage` is indexed by the
+row of the current batch: :meth:`VerifyStage.stage` copies the batch's trees out of the store, derives the tables the
+verify kernels read (masks, window codes, context lengths, slot-indexed parents and depths) and moves each draft
+row's position from its place in the flattened chain to ``context + depth``. One gfx950 launch does all of it
+(``csrc/tree_tables.hip``). Rows of a tree are ordered so a parent precedes its children; a prefix of the rows is a
+tree of its own.
 """
 
 from __future__ import annotations
@@ -13,8 +16,8 @@ import torch
 
 from eagle_harness.kernels import _native
 
-# The conv window of the root reads the request's conv state: codes -1, -2, -3 are the last, second to last and
-# third to last entry of the window before the root.
+# Negative window codes name the columns of the request's saved conv history: the root's parent is -1 (the newest
+# saved input), its grandparent -2, and -3 is the oldest of the three.
 WINDOW_CODES = (-1, -2, -3)
 
 
@@ -64,8 +67,9 @@ def stage_tree(
 
 
 class TreeStore:
-    """The tree of each request by request state slot: ``parents`` (written by the drafter) and the accepted
-    ``path`` (root first, ``path_len`` rows) the walk writes (vllm/verify_layout.py:89-97)."""
+    """Per request state slot (vllm/verify_layout.py:89-97): ``parents`` [slots, W] int32 as the drafter leaves them
+    (row 0 holds -1), and the accept walk's result, ``path`` [slots, W] (accepted rows from the root) with
+    ``path_len`` [slots] valid entries."""
 
     def __init__(self, max_reqs: int, width: int, device: torch.device):
         self.width = width
@@ -75,7 +79,9 @@ class TreeStore:
 
 
 class VerifyStage:
-    """The batch's trees, by batch row (vllm/verify_layout.py:100-190)."""
+    """Per batch row (vllm/verify_layout.py:100-190): the tables the verify layers read during one forward, plus
+    ``state_slots``, the GDN slot rows a linear-attention layer copies in during the forward so that a graph replay
+    refreshes them as well."""
 
     def __init__(self, max_reqs: int, max_tokens: int, width: int, device: torch.device):
         if width > 64:
@@ -94,11 +100,14 @@ class VerifyStage:
 
     @property
     def verifying(self) -> bool:
-        """Whether the target's layers take the tree path now: a tree is staged, or a graph is being captured."""
+        """True when the layers must run their tree kernels: after a tree was staged, and always while the current
+        stream captures a graph (a capture records only the kernels it runs, and the verify graphs are captured
+        with no batch staged)."""
         return self.active or torch.cuda.is_current_stream_capturing()
 
     def publish_slots_of(self, layer_name: str) -> torch.Tensor:
-        """The buffer a linear-attention layer (one per KV cache group) publishes its group's slots to."""
+        """Allocates (or replaces) the [max_reqs, W] int32 table into which the layer ``layer_name``, the one chosen
+        per KV cache group, copies its group's state slots."""
         buf = self.state_slots[layer_name] = torch.zeros(self.max_reqs, self.width, dtype=torch.int32, device=self.device)
         return buf
 
@@ -115,8 +124,11 @@ class VerifyStage:
         tree: bool,
         model_positions: torch.Tensor | None = None,
     ) -> None:
-        """Gather the batch's trees from ``store`` and turn ``positions`` from chain to depth positions
-        (``tree=False``: stage chains and leave the positions)."""
+        """Fills this stage from ``store`` for the batch described by ``idx_mapping`` / ``query_start_loc`` /
+        ``cu_num_logits`` and rewrites ``positions`` in place to tree positions; the chain positions are kept for
+        :meth:`restore_positions`. With ``tree=False`` every request is staged as a chain and ``positions`` keep
+        their values. ``model_positions``, when the model reads positions from a separate (e.g. multi-row)
+        tensor, is shifted by the same per-token amounts."""
         self.chain_positions[:num_tokens].copy_(positions[:num_tokens])
         stage_tree(
             store.parents,
@@ -138,7 +150,7 @@ class VerifyStage:
             model_positions[:, :num_tokens] += positions[:num_tokens] - self.chain_positions[:num_tokens]
 
     def restore_positions(self, positions: torch.Tensor, num_tokens: int) -> None:
-        """Put the chain positions back after the verify forward."""
+        """Writes the saved chain positions back into ``positions`` (a no-op when chains were staged)."""
         if self.active:
             positions[:num_tokens].copy_(self.chain_positions[:num_tokens])
 
@@ -152,5 +164,5 @@ def set_stage(stage: VerifyStage | None) -> None:
 
 
 def get_stage() -> VerifyStage | None:
-    """The process's verify stage; ``None`` while no speculator is running."""
+    """The stage registered by :func:`set_stage`, or ``None``."""
     return _STAGE
