@@ -23,6 +23,7 @@ LIBRARY = Path(__file__).resolve().parent / "libeagle4_amd.so"
 
 OK = 0
 NOT_COVERED = -1
+SCRATCH_TOO_SMALL = -2
 
 BF16, F16, F32, FP8_E4M3, I32, I64, U8 = range(7)
 _DTYPE_CODES = {
@@ -222,6 +223,7 @@ ENTRIES = {
     "eagle4_gdn_tree_records_update": (RecordsArgs, 5),
     "eagle4_gdn_tree_records_commit": (RecordsCommitArgs, 6),
     "eagle4_verify_attention": (AttnArgs, 7),
+    "eagle4_verify_attention_static": (AttnArgs, 7),
     "eagle4_argmax_rows": (ArgmaxArgs, 8),
     "eagle4_accept_tree": (AcceptTreeArgs, 9),
     "eagle4_accept_tail": (AcceptTailArgs, 10),
@@ -232,7 +234,8 @@ ENTRIES = {
     "eagle4_row_attention": (RowAttnArgs, 15),
     "eagle4_mamba2_tree_state_update": (Mamba2Args, 16),
 }
-EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_version", "eagle4_args_size")
+EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_verify_attention_static_bytes", "eagle4_version",
+                 "eagle4_args_size")
 
 
 @functools.lru_cache(maxsize=None)
@@ -257,6 +260,8 @@ def library() -> ctypes.CDLL:
             raise RuntimeError(f"eagle4_amd: {struct.__name__} is {ctypes.sizeof(struct)} bytes here, {native} in {path}")
     lib.eagle4_verify_attention_workspace.argtypes = [ctypes.POINTER(AttnArgs)]
     lib.eagle4_verify_attention_workspace.restype = ctypes.c_int64
+    lib.eagle4_verify_attention_static_bytes.argtypes = []
+    lib.eagle4_verify_attention_static_bytes.restype = ctypes.c_int64
     return lib
 
 
@@ -273,5 +278,8 @@ def launch(name: str, args: ctypes.Structure, device: torch.device) -> None:
         status = fn(ctypes.byref(args), ctypes.c_void_p(stream_of(device)))
     if status == NOT_COVERED:
         raise NotCovered(f"eagle4_amd: {name} does not cover this launch (shape, dtype or layout)")
+    if status == SCRATCH_TOO_SMALL:
+        raise ValueError(f"eagle4_amd: {name} needs more scratch than its static buffer holds "
+                         f"({library().eagle4_verify_attention_static_bytes()} bytes); nothing was launched")
     if status != OK:
         raise RuntimeError(f"eagle4_amd: {name} failed with HIP error {status}")

@@ -44,6 +44,7 @@ def verify_attention(
     k_scale: Optional[torch.Tensor] = None,
     v_scale: Optional[torch.Tensor] = None,
     chunk: int = 0,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """Tree verify attention into ``out`` ``[tokens, Hq, D]`` (rows past the last request's are left alone;
     vllm/verify_attention.py:142-207).
@@ -54,7 +55,9 @@ def verify_attention(
     ``j`` is row ``r`` or one of its ancestors. Every request has at most ``max_query_len`` (<= 64) rows.
     ``k_scale`` / ``v_scale``: fp32 ``[blocks, Hkv]`` scales of an fp8-e4m3 cache. ``chunk``: context keys per split
     of the split-context schedule (a multiple of 64; 0 lets the library choose the streamed schedule where it
-    applies).
+    applies). ``no_alloc``: allocate nothing; the split partials go to the
+    library's static per-GPU buffer (``eagle4_verify_attention_static``, 64 MiB), and a launch needing more raises
+    ValueError before anything runs. Every such call on one GPU shares that buffer: calls overlapping in time race.
     """
     num_reqs = query_start_loc.shape[0] - 1
     heads, head_dim = q.shape[1], q.shape[2]
@@ -128,6 +131,9 @@ def verify_attention(
     if q.dtype != out.dtype or q.dtype != k_new.dtype or q.dtype != v_new.dtype:
         raise _native.NotCovered("q, k_new, v_new and out must share a dtype (bf16, fp16, or fp32 over fp32 pages)")
     lib = _native.library()
+    if no_alloc:
+        _native.launch("eagle4_verify_attention_static", args, q.device)
+        return out
     need = lib.eagle4_verify_attention_workspace(args)
     if need < 0:
         raise _native.NotCovered("eagle4_amd: verify_attention does not cover this launch (shape, dtype or layout)")

@@ -31,6 +31,7 @@ extern "C" {
 
 #define EAGLE4_OK 0
 #define EAGLE4_NOT_COVERED (-1)
+#define EAGLE4_SCRATCH_TOO_SMALL (-2) /* eagle4_verify_attention_static: the launch needs more than its static scratch */
 
 #define EAGLE4_BF16 0
 #define EAGLE4_F16 1
@@ -244,6 +245,16 @@ typedef struct eagle4_attn_args {
 } eagle4_attn_args;
 int64_t eagle4_verify_attention_workspace(const eagle4_attn_args* args);
 int eagle4_verify_attention(const eagle4_attn_args* args, void* stream);
+
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops or harnesses that forbid hipMalloc): eagle4_verify_attention with its split partials in a static
+ * per-GPU device buffer of eagle4_verify_attention_static_bytes() (64 MiB) instead of a caller workspace;
+ * args->workspace / workspace_bytes are ignored. Same kernels and results as eagle4_verify_attention. Returns
+ * EAGLE4_SCRATCH_TOO_SMALL, launching nothing, when eagle4_verify_attention_workspace(args) exceeds the buffer.
+ * Allocates nothing. Call with the stream's device current. The buffer keeps the last call's contents and is shared
+ * by every call on that GPU: calls that overlap in time on one GPU race. */
+int64_t eagle4_verify_attention_static_bytes(void);
+int eagle4_verify_attention_static(const eagle4_attn_args* args, void* stream);
 
 /* ---- greedy accept: vllm/tree_accept.py:45-115 (walk), :195-216 (argmax of the greedy sampler) --------------------- */
 typedef struct eagle4_argmax_args {
