@@ -445,6 +445,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--records-only", action="store_true", help="time only the records chunk form and print it")
     ap.add_argument("--rows-only", action="store_true", help="time only the rows outside the step and print them")
+    ap.add_argument("--step-only", action="store_true",
+                    help="time only the verify step (no records chunk, no rows); for quick comparisons")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -635,8 +637,9 @@ def main() -> int:
         "kernels": kernels,
         "cpu_baseline": _cpu_baseline(work, args.cpu_sample, args.cpu_seconds) if work is not None else None,
     }
-    result["records_chunk"] = _records_chunk(args.steps)
-    result["rows"] = _rows(args.steps)
+    if not args.step_only:
+        result["records_chunk"] = _records_chunk(args.steps)
+        result["rows"] = _rows(args.steps)
     print(json.dumps(result), flush=True)
     return 0
 

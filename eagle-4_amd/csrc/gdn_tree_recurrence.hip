@@ -3,8 +3,8 @@
 // Roofline: HBM writes. Every node of every (request, value head) writes its whole [V, K] state snapshot (64 KB in
 // fp32 at V = K = 128) and reads ~1 KB of inputs, at ~1.7 FLOP per byte. The layout is chosen for the stores:
 //
-//  * A workgroup is one wave and owns one (V tile, request, value head); the tile's state lives in VGPRs for the
-//    whole walk.
+//  * A workgroup owns one (V tile, request, value head); the tile's state lives in the VGPRs of its waves for the
+//    whole walk, each wave owning RPT x (64 / C) rows.
 //  * C adjacent lanes share a V row, each holding E = K / C state values as E/4 float4 chunks at k = 4c + 4Cj
 //    (c = lane % C, j = chunk). At K = 128, C = 8: one store instruction writes 8 rows x 128 contiguous bytes, so
 //    every snapshot store is whole 128-byte lines, streamed once.
@@ -23,14 +23,32 @@
 // reload its snapshot from HBM, as the reference does. Any other request keeps the reference's index-order walk
 // with its reloads (the same wave wrote the snapshot it reads: same addresses, same lane, so no barrier is needed).
 //
-// The math and its order follow the walk: h *= exp(g); v' = (v - h k) * beta; h += k v'; o = h q, with beta
-// rounded through b's dtype and q, k L2-normalised with 1e-6 inside the square root.
+// The math and its order follow the walk: h *= exp(g); v' = (v - h k^) * beta; h += k^ v'; o = h q^, with beta
+// rounded through b's dtype and q^ = q scale / |q|, k^ = k / |k| (1e-6 inside the square roots), normalised once per
+// node in the prologue and kept in LDS as fp32.
 
 #include "gdn_walk.h"
 
 namespace {
 
 using namespace e4walk;
+
+// A node's inputs as a lane holds them: its E values of q^ and k^ (fp32), v of its RPT rows (raw), decay and beta.
+template <int E, int RPT, typename IS>
+struct NodeIn {
+  float q[E], k[E];
+  IS v[RPT];
+  float decay, beta;
+};
+
+// Workgroup id -> (request, value head, V tile), the tile fastest: the workgroups of one request are adjacent, so the
+// resident ones write a few requests' slot runs at a time. (Handing each XCD whole requests measured slower.)
+E4_DEV void item_of(int id, int HV, int tiles, int& n, int& hv, int& tile) {
+  const int G = tiles * HV;
+  n = id / G;
+  hv = (id % G) / tiles;
+  tile = id % tiles;
+}
 
 // Workgroup: WAVES waves over consecutive V rows of one (request, value head); each wave owns RPT x (64 / C) rows.
 // The request's first TS nodes are staged in LDS up front (q, k, the workgroup's v rows, and the node scalars), so the
@@ -48,21 +66,23 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   using SS = typename Tsnap::storage;
   constexpr int TS = sizeof(IS) == 4 ? 8 : 16;  // staged nodes
   constexpr bool kExact = sizeof(SS) == 4;      // fp32 snapshots: a reload gives the registers bit for bit
-  __shared__ float4 stack[WAVES][S][RPT * NJ][64];
-  __shared__ __align__(16) IS s_q[TS][K];
-  __shared__ __align__(16) IS s_k[TS][K];
+  // The parked-state stack; in the prologue, before any state is parked, it holds the staged nodes' raw q and k rows.
+  constexpr int kStackBytes = WAVES * S * RPT * NJ * 64 * 16;
+  constexpr int kRawBytes = 2 * TS * K * static_cast<int>(sizeof(IS));
+  __shared__ __align__(16) char s_stack[kStackBytes > kRawBytes ? kStackBytes : kRawBytes];
+  __shared__ __align__(16) float s_q[TS][K];  // q^ and k^ of the staged nodes
+  __shared__ __align__(16) float s_k[TS][K];
   __shared__ IS s_v[TS][ROWS];
-  __shared__ float4 s_sc[TS];
+  __shared__ float4 s_sc[TS];  // decay, beta, scale / |q|, 1 / |k|
+  auto& s_qr = *reinterpret_cast<IS(*)[TS][K]>(s_stack);
+  auto& s_kr = *reinterpret_cast<IS(*)[TS][K]>(s_stack + TS * K * sizeof(IS));
 
-#ifdef E4_GDN_N_FAST
-  const int n = blockIdx.y, hv = blockIdx.z;
-#else
-  const int n = blockIdx.z, hv = blockIdx.y;
-#endif
+  int n, hv, tile;
+  item_of(blockIdx.x, a.HV, (a.V + ROWS - 1) / ROWS, n, hv, tile);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane % C, rr = lane / C;
   const int ih = hv / (a.HV / a.H);
-  const int row0 = blockIdx.x * ROWS;
+  const int row0 = tile * ROWS;
   int rows[RPT], lrow[RPT];
 #pragma unroll
   for (int s = 0; s < RPT; ++s) {
@@ -70,7 +90,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     rows[s] = row0 + lrow[s];
   }
 
-  if (a.publish != nullptr && blockIdx.x == 0 && hv == 0) {  // _publish_slot_table (:188-200)
+  if (a.publish != nullptr && tile == 0 && hv == 0) {  // _publish_slot_table (:188-200)
     for (int i = tid; i < a.num_slot_cols; i += NT)
       a.publish[n * a.stride_publish + i] = static_cast<int32_t>(e4::ld(a.snap_indices, n, i));
   }
@@ -135,55 +155,75 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   // ---- staging: q, k, v and the node scalars of nodes [0, ts) into LDS --------------------------------------------
   const float A = -expf(widen_raw(A_raw, a.A_log_dtype));
   const float dt_bias = widen_raw(dt_raw, a.dt_bias_dtype);
-  stg.commit(s_q, s_k, s_v, s_sc, ts, tid, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
+  stg.commit(s_qr, s_kr, s_v, s_sc, ts, tid, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
 #pragma unroll
   for (int s = 0; s < RPT; ++s)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) widen_state_raw(h0raw[s][j], a.h0_dtype, &h[s][4 * j]);
   __syncthreads();
-  stage_norms<Tin, K, TS, NT>(s_q, s_k, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
+  stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
   __syncthreads();
+  for (int i = tid; i < ts * K; i += NT) {  // q^ and k^, read by every node of the walk
+    const int t = i / K, e = i % K;
+    const float4 sc = s_sc[t];
+    s_q[t][e] = Tin::to_f32(s_qr[t][e]) * sc.z;
+    s_k[t][e] = Tin::to_f32(s_kr[t][e]) * sc.w;
+  }
+  __syncthreads();  // the raw rows' space becomes the stack
 
   settle_loads();  // the initial state and the plan tables
-  // A node's inputs: staged ones from LDS, later ones (T > TS) from global memory with their scalars computed here.
-  auto fetch = [&](Node<E, RPT, Tin>& nd, int u) {
+  // A node's inputs: staged nodes from LDS, later ones (T > TS) from global memory with their scalars computed here.
+  auto fetch = [&](NodeIn<E, RPT, IS>& nd, int u) {
     if (u < TS) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        nd.q[j] = *reinterpret_cast<const Raw4<Tin>*>(&s_q[u][4 * c + 4 * C * j]);
-        nd.k[j] = *reinterpret_cast<const Raw4<Tin>*>(&s_k[u][4 * c + 4 * C * j]);
+        const float4 q4 = *reinterpret_cast<const float4*>(&s_q[u][4 * c + 4 * C * j]);
+        const float4 k4 = *reinterpret_cast<const float4*>(&s_k[u][4 * c + 4 * C * j]);
+        nd.q[4 * j] = q4.x, nd.q[4 * j + 1] = q4.y, nd.q[4 * j + 2] = q4.z, nd.q[4 * j + 3] = q4.w;
+        nd.k[4 * j] = k4.x, nd.k[4 * j + 1] = k4.y, nd.k[4 * j + 2] = k4.z, nd.k[4 * j + 3] = k4.w;
       }
 #pragma unroll
       for (int s = 0; s < RPT; ++s) nd.v[s] = s_v[u][lrow[s]];
-      nd.sc = s_sc[u];
+      const float4 sc = s_sc[u];
+      nd.decay = sc.x;
+      nd.beta = sc.y;
     } else {
       const int64_t tok = bos + u;
       const IS* q = static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K;
-      const IS* k = static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K;
-      float qq = 0.f, kk = 0.f;
+      const IS* kp = static_cast<const IS*>(a.k) + tok * a.stride_k + static_cast<int64_t>(ih) * K;
+      Raw4<Tin> qr[NJ], kr[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        nd.q[j] = *reinterpret_cast<const Raw4<Tin>*>(q + 4 * c + 4 * C * j);
-        nd.k[j] = *reinterpret_cast<const Raw4<Tin>*>(k + 4 * c + 4 * C * j);
-        float qf[4], kf[4];
-        widen4<Tin>(nd.q[j], qf);
-        widen4<Tin>(nd.k[j], kf);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          qq = fmaf(qf[e], qf[e], qq);
-          kk = fmaf(kf[e], kf[e], kk);
-        }
+        qr[j] = *reinterpret_cast<const Raw4<Tin>*>(q + 4 * c + 4 * C * j);
+        kr[j] = *reinterpret_cast<const Raw4<Tin>*>(kp + 4 * c + 4 * C * j);
       }
-      qq = e4::group_sum<C>(qq);
-      kk = e4::group_sum<C>(kk);
       const IS* v = static_cast<const IS*>(a.v) + tok * a.stride_v + static_cast<int64_t>(hv) * a.V;
 #pragma unroll
       for (int s = 0; s < RPT; ++s) nd.v[s] = v[rows[s] < a.V ? rows[s] : a.V - 1];
-      const float2 g = gate_of(load_raw(a.a, tok * a.stride_a + hv, a.gate_dtype),
-                               load_raw(a.b, tok * a.stride_b + hv, a.gate_dtype), a.gate_dtype,
-                               a.softplus_beta, a.softplus_threshold, A, dt_bias);
-      nd.sc = make_float4(g.x, g.y, a.scale / sqrtf(qq + 1e-6f), 1.0f / sqrtf(kk + 1e-6f));
+      const uint32_t ga = load_raw(a.a, tok * a.stride_a + hv, a.gate_dtype);
+      const uint32_t gb = load_raw(a.b, tok * a.stride_b + hv, a.gate_dtype);
       settle_loads();
+      float qq = 0.f, kk = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        widen4<Tin>(qr[j], &nd.q[4 * j]);
+        widen4<Tin>(kr[j], &nd.k[4 * j]);
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        qq = fmaf(nd.q[e], nd.q[e], qq);
+        kk = fmaf(nd.k[e], nd.k[e], kk);
+      }
+      const float qs = a.scale / sqrtf(e4::group_sum<C>(qq) + 1e-6f);
+      const float ks = 1.0f / sqrtf(e4::group_sum<C>(kk) + 1e-6f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        nd.q[e] *= qs;
+        nd.k[e] *= ks;
+      }
+      const float2 g = gate_of(ga, gb, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
+      nd.decay = g.x;
+      nd.beta = g.y;
     }
   };
 
@@ -201,9 +241,10 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
         if (rows[s] < a.V) load4<Tsnap>(src + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
     settle_loads();
   };
-  float4 (*const my_stack)[RPT * NJ][64] = stack[wave];
+  float4 (*const my_stack)[RPT * NJ][64] = reinterpret_cast<float4 (*)[S][RPT * NJ][64]>(s_stack)[wave];
+  const bool full_tile = row0 + ROWS <= a.V;  // every row of the tile exists: stores need no row predicate
 
-  Node<E, RPT, Tin> cur, nxt;
+  NodeIn<E, RPT, IS> cur, nxt;
   fetch(cur, 0);
   int u = 0, sp = 0;
   uint64_t unparked = 0;  // nodes with several children that found the stack full
@@ -233,31 +274,23 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     }
     if (next >= 0 && next < TS) fetch(nxt, next);  // staged: LDS reads only, ahead of their use
 
-    // the delta rule step (:167-185) with the normalisation folded into the dot products and the update:
-    // h k^ = ks (h k), k^ dv = k (ks dv), o = qs (h q)
-    const float decay = cur.sc.x, beta = cur.sc.y, qs = cur.sc.z, ks = cur.sc.w;
-    const float dks = decay * ks;
-    float qf[E], kf[E];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      widen4<Tin>(cur.q[j], &qf[4 * j]);
-      widen4<Tin>(cur.k[j], &kf[4 * j]);
-    }
+    // the delta rule step (:167-185): h *= decay; v' = (v - h k^) beta; h += k^ v'; o = h q^
+    const float decay = cur.decay, beta = cur.beta;
     float o[RPT];
 #pragma unroll
     for (int s = 0; s < RPT; ++s) {
       float hk = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) hk = fmaf(h[s][e], kf[e], hk);
+      for (int e = 0; e < E; ++e) hk = fmaf(h[s][e], cur.k[e], hk);
       hk = e4::group_sum<C>(hk);
-      const float kdv = (Tin::to_f32(cur.v[s]) - hk * dks) * beta * ks;
+      const float dv = (Tin::to_f32(cur.v[s]) - hk * decay) * beta;
       float hq = 0.f;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        h[s][e] = fmaf(kf[e], kdv, h[s][e] * decay);
-        hq = fmaf(h[s][e], qf[e], hq);
+        h[s][e] = fmaf(cur.k[e], dv, h[s][e] * decay);
+        hq = fmaf(h[s][e], cur.q[e], hq);
       }
-      o[s] = e4::group_sum<C>(hq) * qs;
+      o[s] = e4::group_sum<C>(hq);
     }
     const int64_t t = bos + u;
     if (c == 0) {
@@ -276,11 +309,19 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     }
     if (slot > a.pad_slot_id) {
       SS* dst = snap_at(slot, u);
+      if (full_tile) {
 #pragma unroll
-      for (int j = 0; j < NJ; ++j)
+        for (int j = 0; j < NJ; ++j)
 #pragma unroll
-        for (int s = 0; s < RPT; ++s)
-          if (rows[s] < a.V) store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+          for (int s = 0; s < RPT; ++s)
+            store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int s = 0; s < RPT; ++s)
+            if (rows[s] < a.V) store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+      }
     }
 
     // the state the next node starts from
@@ -352,11 +393,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
 template <int K, int C, int RPT, int WAVES, int S, typename Tin>
 int launch_snap(const eagle4_gdn_args& a, hipStream_t s) {
   constexpr int ROWS = WAVES * RPT * (64 / C);
-#ifdef E4_GDN_N_FAST
-  const dim3 grid(e4::ceil_div(a.V, ROWS), a.N, a.HV);
-#else
-  const dim3 grid(e4::ceil_div(a.V, ROWS), a.HV, a.N);
-#endif
+  const dim3 grid(e4::ceil_div(a.V, ROWS) * a.HV * a.N);
   if (a.snap_dtype == EAGLE4_F32)
     gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_BF16)
@@ -390,20 +427,13 @@ extern "C" int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* a, void* 
   if (a->stride_q % 4 || a->stride_k % 4 || a->stride_v % 4 || reinterpret_cast<uintptr_t>(a->q) % (4 * esz) ||
       reinterpret_cast<uintptr_t>(a->k) % (4 * esz) || reinterpret_cast<uintptr_t>(a->v) % (4 * esz))
     return EAGLE4_NOT_COVERED;
-  // 4 waves per workgroup; up to 16 state values per lane and stack slot (16 KB of LDS per slot and workgroup)
+  // 4 waves per workgroup; up to 16 state values per lane and stack slot
   switch (a->K) {
     case 8: return launch_in<8, 2, 1, 4, 4>(*a, s);
     case 16: return launch_in<16, 4, 1, 4, 4>(*a, s);
     case 32: return launch_in<32, 8, 1, 4, 4>(*a, s);
     case 64: return launch_in<64, 8, 1, 4, 4>(*a, s);
-#ifndef E4_GDN_RPT
-#define E4_GDN_RPT 2
-#define E4_GDN_S 2
-#endif
-#ifndef E4_GDN_WAVES
-#define E4_GDN_WAVES 4
-#endif
-    case 128: return launch_in<128, 8, E4_GDN_RPT, E4_GDN_WAVES, E4_GDN_S>(*a, s);
+    case 128: return launch_in<128, 8, 1, 4, 2>(*a, s);
     case 256: return launch_in<256, 16, 1, 4, 2>(*a, s);
     default: return EAGLE4_NOT_COVERED;
   }
