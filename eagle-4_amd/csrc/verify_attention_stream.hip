@@ -723,18 +723,18 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   bool row_ok = false;
   int t = 0, head = 0;
   // the segment's row of this lane: Q, ancestor mask
-  auto enter = [&](const Cursor& c) {
+  auto enter = [&](const Cursor& c, uint4 (&qr)[D / 32], int64_t& mask_r, bool& ok_r, int& t_r, int& head_r) {
     const int kvh = c.k / RG, rg = c.k - kvh * RG;
     const int rows = c.width < a.max_query_len ? c.width : a.max_query_len;
     const int rt = rg * C + wave;
     const int rho = rt * 16 + l16;
-    t = rho / G;
-    head = kvh * G + (rho - t * G);
-    row_ok = rt < p.row_tiles && t < rows;
-    load_q<D>(q, static_cast<const uint16_t*>(a.q) + (c.qs + t) * a.stride_qt + head * a.stride_qh, row_ok, g);
-    row_mask = row_ok ? a.masks[static_cast<int64_t>(c.b) * a.stride_mask + t] : 0;
+    t_r = rho / G;
+    head_r = kvh * G + (rho - t_r * G);
+    ok_r = rt < p.row_tiles && t_r < rows;
+    load_q<D>(qr, static_cast<const uint16_t*>(a.q) + (c.qs + t_r) * a.stride_qt + head_r * a.stride_qh, ok_r, g);
+    mask_r = ok_r ? a.masks[static_cast<int64_t>(c.b) * a.stride_mask + t_r] : 0;
   };
-  enter(cc);
+  enter(cc, q, row_mask, row_ok, t, head);
   f32x4_t acc[D / 16];
   float mref, lsum;
   auto reset = [&] {
@@ -773,6 +773,20 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
 
     const bool seg_end = cc.j == cc.tiles - 1;
     if (seg_end || x == g1 - 1) {
+      // the next segment's rows first (16-bit pages at D 256; elsewhere the registers are not there): their q / mask
+      // loads go out before this segment's stores, so the wait for them (vmcnt retires in issue order) is not a wait
+      // for the stores
+      constexpr bool kAhead = !FP8 && D == 256;
+      const bool more = x + 1 < g1;
+      Cursor cn = cc;
+      uint4 qn[D / 32];
+      int64_t mask_n = 0;
+      bool ok_n = false;
+      int t_n = 0, head_n = 0;
+      if (kAhead && more) {
+        cur_next<CK>(cn, s_qsl, s_ctx, B, HR);
+        enter(cn, qn, mask_n, ok_n, t_n, head_n);
+      }
       float ls = lsum + __shfl_xor(lsum, 16, 64);
       ls += __shfl_xor(ls, 32, 64);
       if (row_ok) {
@@ -786,9 +800,19 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
           if (g == 0) a.workspace[p.lse_off + part] = ls > 0.f ? mref + log2f(ls) : -INFINITY;
         }
       }
-      if (x + 1 < g1) {
-        cur_next<CK>(cc, s_qsl, s_ctx, B, HR);
-        enter(cc);
+      if (more) {
+        if constexpr (kAhead) {
+          cc = cn;
+#pragma unroll
+          for (int i = 0; i < D / 32; ++i) q[i] = qn[i];
+          row_mask = mask_n;
+          row_ok = ok_n;
+          t = t_n;
+          head = head_n;
+        } else {
+          cur_next<CK>(cc, s_qsl, s_ctx, B, HR);
+          enter(cc, q, row_mask, row_ok, t, head);
+        }
         reset();
         piece_j0 = 0;
       }
@@ -799,11 +823,14 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
 }
 
 // Merges the pieces of each segment cut by share boundaries (vllm/verify_attention.py:115-139): weights
-// 2^(lse_i - max) over the pieces' normalised fp32 partials. A workgroup takes 256 (row, 4 columns) items of one
-// segment, one item per thread, and folds the pieces in one pass with a running max, so a thread's loads do not
-// wait on each other.
+// 2^(lse_i - max) over the pieces' normalised fp32 partials. A thread takes 16 columns of one row and folds the pieces
+// four at a time with a running max, every load of a group of four issued before the first is used.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_args a, const StreamPlan p) {
+  constexpr int kCols = D < 16 ? D : 16;
+  constexpr int TPR = D / kCols;  // threads per row
+  constexpr int NV = kCols / 4;   // float4 per thread and piece
+  constexpr int kGroup = 4;       // pieces in flight
   const int s = blockIdx.x;
   const int b = s / p.HR, k = s - b * p.HR;
   const int64_t* pre = reinterpret_cast<const int64_t*>(a.workspace);
@@ -814,11 +841,10 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
   const int64_t start = pre[b] * p.HR + k * tiles, end = start + tiles;
   const int64_t w0 = ((start + 1) * nact - 1) / tiles_all, w1 = (end * nact - 1) / tiles_all;
   if (w0 == w1) return;  // inside one share: written directly
-  constexpr int TPR = D / 4;
   const int item = blockIdx.y * 256 + threadIdx.x;
   const int rows_seg = p.rows_seg;
   if (item >= rows_seg * TPR) return;
-  const int r = item / TPR, d = 4 * (item % TPR);
+  const int r = item / TPR, d = kCols * (item % TPR);
   const int G = p.G, kvh = k / p.RG, rg = k - kvh * p.RG;
   const int64_t qs = e4::ld(a.query_start_loc, b);
   int64_t rows = e4::ld(a.query_start_loc, b + 1) - qs;
@@ -828,28 +854,48 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
   const int t = rho / G, gq = rho - t * G;
   if (rt >= p.row_tiles || t >= rows) return;
   float mx = -INFINITY, wsum = 0.f;
-  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int64_t wi = w0; wi <= w1; ++wi) {
-    const int64_t part = (s + wi) * rows_seg + r;
-    const float ls = a.workspace[p.lse_off + part];
-    const float4 v = *reinterpret_cast<const float4*>(a.workspace + p.part_off + part * D + d);
-    if (ls == -INFINITY) continue;  // a piece with no visible key
-    const float m_new = fmaxf(mx, ls);
-    const float keep = exp2f(mx - m_new), wt = exp2f(ls - m_new);
-    sum.x = sum.x * keep + wt * v.x;
-    sum.y = sum.y * keep + wt * v.y;
-    sum.z = sum.z * keep + wt * v.z;
-    sum.w = sum.w * keep + wt * v.w;
-    wsum = wsum * keep + wt;
-    mx = m_new;
+  float sum[kCols];
+#pragma unroll
+  for (int c = 0; c < kCols; ++c) sum[c] = 0.f;
+  for (int64_t wg = w0; wg <= w1; wg += kGroup) {
+    float ls[kGroup];
+    float4 v[kGroup][NV];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const bool in = wg + i <= w1;
+      const int64_t part = (s + wg + i) * rows_seg + r;
+      ls[i] = in ? a.workspace[p.lse_off + part] : -INFINITY;
+#pragma unroll
+      for (int c = 0; c < NV; ++c)
+        v[i][c] = in ? *reinterpret_cast<const float4*>(a.workspace + p.part_off + part * D + d + 4 * c)
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      if (ls[i] == -INFINITY) continue;  // past the last piece, or a piece with no visible key
+      const float m_new = fmaxf(mx, ls[i]);
+      const float keep = exp2f(mx - m_new), wt = exp2f(ls[i] - m_new);
+#pragma unroll
+      for (int c = 0; c < NV; ++c) {
+        sum[4 * c] = sum[4 * c] * keep + wt * v[i][c].x;
+        sum[4 * c + 1] = sum[4 * c + 1] * keep + wt * v[i][c].y;
+        sum[4 * c + 2] = sum[4 * c + 2] * keep + wt * v[i][c].z;
+        sum[4 * c + 3] = sum[4 * c + 3] * keep + wt * v[i][c].w;
+      }
+      wsum = wsum * keep + wt;
+      mx = m_new;
+    }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-  uint2 o;
-  o.x = pack2<T>(sum.x * inv, sum.y * inv);
-  o.y = pack2<T>(sum.z * inv, sum.w * inv);
-  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + (qs + t) * a.stride_ot +
-                            (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d) = o;
+  uint16_t* orow = static_cast<uint16_t*>(a.out) + (qs + t) * a.stride_ot +
+                   (static_cast<int64_t>(kvh) * G + gq) * a.stride_oh + d;
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    uint2 o;
+    o.x = pack2<T>(sum[4 * c] * inv, sum[4 * c + 1] * inv);
+    o.y = pack2<T>(sum[4 * c + 2] * inv, sum[4 * c + 3] * inv);
+    *reinterpret_cast<uint2*>(orow + 4 * c) = o;
+  }
 }
 
 template <int D, int C, typename T, bool FP8>
@@ -872,8 +918,10 @@ int resident_groups() {
 template <int D, int C, typename T, bool FP8>
 int launch(const eagle4_attn_args& a, const StreamPlan& p, hipStream_t s) {
   verify_stream_kernel<D, C, T, FP8><<<p.nwg, 64 * (C + kProducers), 0, s>>>(a, p);
-  verify_stream_merge<D, T><<<dim3(a.num_reqs * p.HR, e4::ceil_div(static_cast<int64_t>(p.rows_seg) * (D / 4), 256)), 256, 0,
-                               s>>>(a, p);
+  constexpr int kMergeThreadsPerRow = D / (D < 16 ? D : 16);
+  verify_stream_merge<D, T><<<dim3(a.num_reqs * p.HR,
+                                   e4::ceil_div(static_cast<int64_t>(p.rows_seg) * kMergeThreadsPerRow, 256)),
+                              256, 0, s>>>(a, p);
   return E4_LAUNCH_STATUS();
 }
 

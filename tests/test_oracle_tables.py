@@ -145,6 +145,36 @@ def test_ancestors_pad_rows_keep_parents_and_follow_them():
     _check_paths(parents, paths[0], 5)
 
 
+@pytest.mark.parametrize("num_tokens", [1, 2, 5, 11, 15])
+def test_paths_of_a_partial_request(num_tokens):
+    """A request verifying fewer rows than the tree width (num_tokens < width): the path table is the one of the
+    tree's first num_tokens rows (a prefix of a parent-first tree is a tree), checked against that truncated tree's
+    own leaves, root paths and first-child runs; the remaining rows have length 0."""
+    rng = np.random.default_rng(num_tokens)
+    width = 16
+    for _ in range(5):
+        parents = [-1] + [int(rng.integers(0, i)) for i in range(1, width)]
+        paths = np.full((width, 2 + width), 99, np.int32)
+        ot._gdn_tree_paths(parents, num_tokens, width, paths)
+        _check_paths(parents[:num_tokens], paths, width)
+        # and through the public entry with a query_start_loc that gives the request num_tokens rows
+        first, sibling = [-1] * width, [-1] * width
+        last = {}
+        for node in range(1, width):
+            p = parents[node]
+            if p in last:
+                sibling[last[p]] = node
+            else:
+                first[p] = node
+            last[p] = node
+        par = np.zeros((1, width), np.int64)
+        anc = np.zeros((1, 3, width), np.int32)
+        table = np.full((1, width, 2 + width), 99, np.int32)
+        ot.gdn_tree_ancestors(np.array([first]), np.array([sibling]), par, np.array([0]), width, anc,
+                              np.array([0, num_tokens]), table)
+        _check_paths(parents[:num_tokens], table[0], width)
+
+
 def test_paths_sanitise_forward_parents():
     """Parents that are not ancestor-first are replaced by node - 1 so the table stays in bounds (:57-61)."""
     paths = np.zeros((4, 6), np.int32)
