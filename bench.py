@@ -34,6 +34,18 @@ HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s (published)
 METRIC = "verified tree tokens/s (tree-attn+GDN) at B=64, T=16; % of HBM roofline"
 
 
+def _gdn_layer_bytes(B: int, W: int, H: int, HV: int, K: int, V: int, dim: int, path_len, path_last) -> dict:
+    """Algorithmic bytes of one GDN layer's verify (conv, snapshot walk) and of its accepted-path commit."""
+    state = HV * K * V * 4
+    tokens = B * W
+    conv = tokens * dim * 2 * 2 + B * dim * 3 * 2 + B * dim * (W + 2) * 2 + dim * 4 * 2
+    rec = (B * state + tokens * state + tokens * H * K * 2 * 2 + tokens * HV * V * 2 + tokens * HV * 2 * 2
+           + tokens * HV * V * 2 + tokens * 4)
+    moved = sum(1 for n, last in zip(path_len, path_last) if last != n - 1)
+    commit = moved * 2 * state + sum(2 * max(n - 1, 0) for n in path_len) * dim * 2
+    return {"conv": conv, "recurrence": rec, "commit": commit}
+
+
 def _algorithmic_bytes(B, W, att, gdn, ctx, path_len, path_last):
     """Bytes each kernel must move at least (every element once; re-reads and partials not counted)."""
     import math
@@ -42,15 +54,9 @@ def _algorithmic_bytes(B, W, att, gdn, ctx, path_len, path_last):
     kv = sum(int(L) for L in ctx) * att["hkv"] * att["d"] * 2 * 2
     pages = sum(math.ceil(int(L) / att["page"]) for L in ctx) * 4
     attn = kv + pages + tokens * att["hq"] * att["d"] * 2 * 2 + tokens * att["hkv"] * att["d"] * 2 * 2 + B * W * 8
-    H, HV, K, V, dim = gdn["h"], gdn["hv"], gdn["k"], gdn["v"], gdn["dim"]
-    state = HV * K * V * 4
-    rec = B * state + tokens * state + tokens * H * K * 2 * 2 + tokens * HV * V * 2 + tokens * HV * 2 * 2
-    rec += tokens * HV * V * 2 + tokens * 4
-    conv = tokens * dim * 2 * 2 + B * dim * 3 * 2 + B * dim * (W + 2) * 2 + dim * 4 * 2
-    moved = sum(1 for n, last in zip(path_len, path_last) if last != n - 1)
-    commit = moved * 2 * state + sum(2 * max(n - 1, 0) for n in path_len) * dim * 2
+    layer = _gdn_layer_bytes(B, W, gdn["h"], gdn["hv"], gdn["k"], gdn["v"], gdn["dim"], path_len, path_last)
     stage = B * W * (4 + 12 + 8 + 8 + 8) + B * 4
-    return {"stage": stage, "attention": attn, "conv": conv, "recurrence": rec, "commit": commit}
+    return {"stage": stage, "attention": attn, **layer}
 
 
 def _cpu_baseline(work, sample: int, seconds: float) -> dict:
@@ -106,14 +112,25 @@ def _cpu_baseline(work, sample: int, seconds: float) -> dict:
 RECORDS_PUBLISHED_US = {1: 10.5, 4: 11.9, 16: 23.8, 32: 34.7}
 
 
+EAGER = False  # --eager: rows are called without graph capture, so a counter run sees every dispatch
+
+
 def _time_graph(fn, steps: int, reps: int = 5) -> float:
     """Microseconds per call of ``fn``: a HIP graph of ``reps`` calls, replayed ``steps`` times between events on the
-    launch stream, best of 3."""
+    launch stream, best of 3 (with ``EAGER``: ``steps`` plain calls, launch gaps included)."""
     import torch
 
     for _ in range(2):
         fn()
     torch.cuda.synchronize()
+    if EAGER:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(reps):
@@ -415,6 +432,234 @@ def _records_chunk(steps: int) -> dict:
             "speedup_vs_reference": {b: RECORDS_PUBLISHED_US[b] / us[b] for b in us}}
 
 
+def _time_round(fn, steps: int) -> float:
+    """Microseconds per call of ``fn`` (a whole round): a HIP graph of one call, replayed ``steps`` times between
+    events, best of 3. One call per graph, so no part is timed against its own warm caches."""
+    return _time_graph(fn, steps, reps=1)
+
+
+def _configs(steps: int) -> dict:
+    """The configurations beside the metric's step, each timed as whole rounds: the GDN layer at batch 256 (conv,
+    snapshot walk, accepted-path commit), the quantized hybrid round at batch 512 (stage, fp8 attention, three GDN
+    layers, greedy targets over 151936 tokens, tree walk, commit of the three layers), and the records contract's
+    chunk form at batch 64 and 512 with the same heads (bf16 and fp32 pools)."""
+    import math
+
+    import numpy as np
+    import torch
+
+    from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
+    from eagle_harness.kernels.gdn_tree_records import gdn_tree_chunk_update
+    from eagle_harness.kernels.gdn_tree_recurrence import gdn_tree_recurrent_update
+    from eagle_harness.vllm.gdn_tree_verify import LinearStateCommit
+    from eagle_harness.vllm.tree_accept import accept_tree, greedy_targets
+    from eagle_harness.vllm.verify_attention import verify_attention
+    from eagle_harness.vllm.verify_layout import TreeStore, VerifyStage
+    from workloads import ATTN_B512_FP8, GDN_B256, GdnShape, accept_paths, attention_inputs, gdn_inputs, records_inputs
+
+    dev = torch.device("cuda:0")
+    out = {}
+
+    def layer(g, conv_out, rec_out, parents_tab, ancestors):
+        tokens = conv_out.shape[0]
+        H, K = g["q"].shape[2], g["q"].shape[3]
+        HV, V = g["v"].shape[2], g["v"].shape[3]
+        gdn_tree_conv1d_update(g["x"].t()[None], g["conv_state"], g["conv_weight"], None, "silu",
+                               g["slots0"], None, None, ancestors, pad_slot_id=0, out=conv_out.t()[None],
+                               num_accepted_tokens=g["num_accepted"], query_start_loc=g["query_start_loc"])
+        gdn_tree_recurrent_update(g["A_log"], g["dt_bias"], conv_out[:, : H * K].view(1, tokens, H, K),
+                                  conv_out[:, H * K : 2 * H * K].view(1, tokens, H, K),
+                                  conv_out[:, 2 * H * K :].view(1, tokens, HV, V), g["a"], g["b"],
+                                  initial_state_source=g["pool"], initial_state_indices=g["slots"],
+                                  cu_seqlens=g["query_start_loc"], intermediate_states_buffer=g["pool"],
+                                  intermediate_state_indices=g["slots"], retrieve_parent_token=parents_tab,
+                                  num_accepted_tokens=g["num_accepted"], pad_slot_id=0, out=rec_out)
+
+    # configuration 4: one GDN layer at batch 256 x 16 (conv, walk, commit of seeded accepted paths U[1, 12])
+    sh = GDN_B256
+    g = gdn_inputs(sh, seed=6, device=dev, layout="vllm", gen_device=dev)
+    g["slots0"] = g["slots"][:, 0].contiguous()
+    tokens = sh.batch * sh.width
+    conv_out = torch.empty_like(g["x"])
+    rec_out = torch.empty(1, tokens, sh.hv, sh.v, dtype=torch.bfloat16, device=dev)
+    path, plen = accept_paths(g["parents"], 6, sh.width)
+    last = [int(path[b, int(plen[b]) - 1]) for b in range(sh.batch)]
+    path_d, plen_d = path.to(dev), plen.to(dev)
+    idx = torch.arange(sh.batch, dtype=torch.int32, device=dev)
+    commit = LinearStateCommit([(g["conv_state"], g["pool"])], [g["slots"]], dev)
+
+    def round4():
+        layer(g, conv_out, rec_out, g["parent_table"], g["ancestors"])
+        commit.commit(idx, path_d, plen_d)
+
+    us = _time_round(round4, steps)
+    nb = _gdn_layer_bytes(sh.batch, sh.width, sh.h, sh.hv, sh.k, sh.v, g["dim"], plen.tolist(), last)
+    total = sum(nb.values())
+    out["cfg4_gdn_layer_b256x16"] = _row(us, total, verified_tree_tokens_per_s=tokens / (us * 1e-6), parts=nb)
+    del g, conv_out, rec_out, commit
+
+    # configuration 5: the quantized hybrid round at batch 512 x 16: stage, one fp8-e4m3 attention layer (prefixes
+    # U[512, 4096], per-(page, KV head) scales), three GDN layers (conv + walk), greedy targets over 151936 tokens,
+    # the tree walk and the commit of the three layers' accepted states
+    sh5 = GdnShape(512, 16, 16, 32, 128, 128)
+    W5, B5, vocab = sh5.width, sh5.batch, 151936
+    att = attention_inputs(ATTN_B512_FP8, seed=9, device=dev, fp8=True, gen_device=dev)
+    layers = []
+    for li in range(3):
+        gl = gdn_inputs(sh5, seed=9, device=dev, layout="vllm", gen_device=dev)  # the same trees as the attention
+        gl["slots0"] = gl["slots"][:, 0].contiguous()
+        layers.append(gl)
+    assert layers[0]["parents"] == att["parents"]
+    tokens5 = B5 * W5
+    store = TreeStore(B5, W5, dev)
+    store.parents.copy_(torch.tensor(att["parents"], dtype=torch.int32))
+    stage = VerifyStage(B5, tokens5, W5, dev)
+    chain = (att["context_lens"].to(torch.int64)[:, None] + torch.arange(W5, device=dev)).reshape(-1)
+    positions = chain.clone()
+    idx5 = torch.arange(B5, dtype=torch.int32, device=dev)
+    qsl5 = att["query_start_loc"]
+    attn_out = torch.empty_like(att["q"])
+    conv5 = torch.empty_like(layers[0]["x"])
+    rec5 = torch.empty(1, tokens5, sh5.hv, sh5.v, dtype=torch.bfloat16, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    logits = torch.randn(tokens5, vocab, device=dev, generator=gen).bfloat16()
+    target = torch.empty(tokens5, dtype=torch.int64, device=dev)
+    # a node's draft equals its parent's target at 80 % of the nodes (the walk accepts a child whose draft is the
+    # target of the row it hangs from): accepted paths of a few rows
+    greedy_targets(logits, out=target)
+    par = torch.tensor(att["parents"], dtype=torch.int64, device=dev)
+    from_parent = target[(torch.arange(B5, device=dev)[:, None] * W5 + par.clamp(min=0)).reshape(-1)]
+    agree = torch.rand(tokens5, device=dev, generator=gen) < 0.8
+    drafted = torch.where(agree, from_parent, torch.randint(0, vocab, (tokens5,), device=dev, generator=gen))
+    commit5 = LinearStateCommit([(gl["conv_state"], gl["pool"]) for gl in layers], [gl["slots"] for gl in layers], dev)
+
+    def round5():
+        stage.stage(store, idx5, qsl5, qsl5, positions, B5, tokens5, tree=True)
+        verify_attention(att["q"], att["k_new"], att["v_new"], att["key_cache"], att["value_cache"],
+                         att["block_table"], stage.context_lens[:B5], qsl5, stage.masks[:B5], att["scale"], attn_out,
+                         max_query_len=W5, k_scale=att["k_scale"], v_scale=att["v_scale"])
+        for gl in layers:
+            layer(gl, conv5, rec5, stage.parents[:B5], stage.ancestors[:B5])
+        greedy_targets(logits, out=target)
+        accept_tree(target, drafted, qsl5, idx5, store.parents, store)
+        commit5.commit(idx5, store.path, store.path_len)
+        positions.copy_(chain)
+
+    us = _time_round(round5, steps)
+    ctx = att["context_lens"].tolist()
+    pages = sum(math.ceil(L / 16) for L in ctx)
+    attn_b = (sum(ctx) * 4 * 256 * 2 + pages * 4 * 4 * 2 + pages * 4 + tokens5 * 24 * 256 * 2 * 2
+              + tokens5 * 4 * 256 * 2 * 2)
+    plen5 = store.path_len.cpu().tolist()
+    last5 = [int(store.path[b, plen5[b] - 1]) for b in range(B5)]
+    nb5 = _gdn_layer_bytes(B5, W5, sh5.h, sh5.hv, sh5.k, sh5.v, layers[0]["dim"], plen5, last5)
+    parts5 = {"attention_fp8": attn_b, "gdn_layers_x3": 3 * (nb5["conv"] + nb5["recurrence"]),
+              "logits_argmax": logits.numel() * 2 + tokens5 * 8, "commit_x3": 3 * nb5["commit"]}
+    out["cfg5_hybrid_round_b512x16"] = _row(us, sum(parts5.values()), verified_tree_tokens_per_s=tokens5 / (us * 1e-6),
+                                            parts=parts5, accepted_mean=float(np.mean(plen5)))
+    del att, layers, logits, commit5
+
+    # the records contract (no per-node snapshots) at the same heads, batch 64 and 512: the chunk form per layer
+    for B in (64, 512):
+        for pool_dtype, pname in ((torch.bfloat16, "bf16"), (torch.float32, "fp32")):
+            x = records_inputs(B, seed=B, device=dev, pool_dtype=pool_dtype, heads=16, value_heads=32)
+
+            def chunk():
+                gdn_tree_chunk_update(x["A_log"], x["dt_bias"], x["q"], x["k"], x["v"], x["a"], x["b"],
+                                      state=x["state"], state_indices=x["state_indices"],
+                                      query_start_loc=x["query_start_loc"], parent=x["parent"], records=x["records"],
+                                      record_indices=x["record_indices"], width=x["width"])
+
+            us = _time_round(chunk, steps)
+            Wr, HV, K, V = x["width"], 32, 128, 128
+            esz = 2 if pool_dtype == torch.bfloat16 else 4
+            nbytes = (B * HV * V * K * esz + B * Wr * HV * (V + K + 1) * 4 + B * Wr * 16 * K * 2 * 2
+                      + B * Wr * HV * V * 2 * 2 + B * Wr * HV * 2 * 2)
+            out[f"records_chunk_b{B}x16_h16_hv32_{pname}_pool"] = _row(us, nbytes)
+            del x
+    return out
+
+
+def _cpu_configs(seconds: float) -> dict:
+    """The oracle (torch on this host's cores) over configurations 1-4: attention fp32 at batch 1, the GDN layer
+    (conv, walk, commit) at batch 1, bf16 attention at batch 64, the GDN layer at batch 256. The batch-64 and -256
+    configurations run on a sample of 8 and 16 requests of their shape (the oracle's cost is linear in requests, so
+    tokens/s carries over). Each is timed in whole passes for at least ``seconds`` (one pass at least)."""
+    import dataclasses
+    import platform
+
+    import torch
+
+    from oracle import attention as oa
+    from oracle import commit as ocm
+    from oracle import conv as oc
+    from oracle import recurrence as orr
+    from workloads import ATTN_B1, ATTN_B64, GDN_B1, GDN_B256, accept_paths, attention_inputs, gdn_inputs
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
+
+    def timed(fn):
+        fn()  # one untimed pass: first-touch allocations and thread-pool start
+        t0 = time.perf_counter()
+        passes = 0
+        while passes == 0 or time.perf_counter() - t0 < seconds:
+            fn()
+            passes += 1
+        return (time.perf_counter() - t0) / passes
+
+    out = {"cores": threads, "cpu_model": model, "kind": "port"}
+    for name, shape, dtype in (("cfg1_attention_fp32_b1", ATTN_B1, torch.float32),
+                               ("cfg3_attention_bf16_b64", dataclasses.replace(ATTN_B64, batch=8), torch.bfloat16)):
+        a = attention_inputs(shape, seed=0, dtype=dtype)
+
+        def attn():
+            oa.verify_attention(a["q"], a["k_new"], a["v_new"], a["key_cache"], a["value_cache"], a["block_table"],
+                                a["context_lens"], a["query_start_loc"], a["masks"], a["scale"],
+                                torch.empty_like(a["q"]), max_query_len=shape.width)
+
+        s = timed(attn)
+        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch,
+                     "verified_tree_tokens_per_s": shape.batch * shape.width / s}
+        del a
+    for name, shape in (("cfg2_gdn_layer_b1", GDN_B1), ("cfg4_gdn_layer_b256", dataclasses.replace(GDN_B256, batch=16))):
+        g = gdn_inputs(shape, seed=0, layout="vllm")
+        path, plen = accept_paths(g["parents"], 0, shape.width)
+        tokens, HK = shape.batch * shape.width, shape.h * shape.k
+        slots0 = g["slots"][:, 0].contiguous()
+        pool0, conv0 = g["pool"].clone(), g["conv_state"].clone()
+
+        def gdn_layer():
+            g["pool"].copy_(pool0)
+            g["conv_state"].copy_(conv0)
+            conv_out = torch.empty_like(g["x"])
+            oc.gdn_tree_conv1d_update(g["x"].t()[None], g["conv_state"], g["conv_weight"], None, "silu", slots0, None,
+                                      None, g["ancestors"], pad_slot_id=0, out=conv_out.t()[None],
+                                      num_accepted_tokens=g["num_accepted"], query_start_loc=g["query_start_loc"])
+            orr.gdn_tree_recurrent_update(g["A_log"], g["dt_bias"], conv_out[:, :HK].reshape(1, tokens, shape.h, shape.k),
+                                          conv_out[:, HK : 2 * HK].reshape(1, tokens, shape.h, shape.k),
+                                          conv_out[:, 2 * HK :].reshape(1, tokens, shape.hv, shape.v), g["a"], g["b"],
+                                          initial_state_source=g["pool"], initial_state_indices=g["slots"],
+                                          cu_seqlens=g["query_start_loc"], intermediate_states_buffer=g["pool"],
+                                          intermediate_state_indices=g["slots"],
+                                          retrieve_parent_token=g["parent_table"],
+                                          num_accepted_tokens=g["num_accepted"], pad_slot_id=0)
+            ocm.linear_state_commit([g["conv_state"]], [g["pool"]], [g["slots"]],
+                                    torch.arange(shape.batch, dtype=torch.int32), path, plen)
+
+        s = timed(gdn_layer)
+        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch, "verified_tree_tokens_per_s": tokens / s,
+                     "note": "the pass restores the state pool and conv state first (two host copies)"}
+        del g, pool0, conv0
+    return out
+
+
 def _calibrate_copy(steps: int) -> None:
     import torch
 
@@ -446,8 +691,16 @@ def main() -> int:
     ap.add_argument("--records-only", action="store_true", help="time only the records chunk form and print it")
     ap.add_argument("--rows-only", action="store_true", help="time only the rows outside the step and print them")
     ap.add_argument("--step-only", action="store_true",
-                    help="time only the verify step (no records chunk, no rows); for quick comparisons")
+                    help="time only the verify step (no records chunk, rows or configurations); for quick comparisons")
+    ap.add_argument("--configs-only", action="store_true", help="time only the configuration rounds and print them")
+    ap.add_argument("--cpu-configs", type=float, default=2.0,
+                    help="seconds per configuration for the oracle's CPU times of configurations 1-4 (0: skip)")
+    ap.add_argument("--eager", action="store_true",
+                    help="rows, records and configurations without graph capture (for counter runs); times include "
+                         "launch gaps")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: the verify path needs no collective and this build runs on a single MI355X "
@@ -463,6 +716,9 @@ def main() -> int:
         return 0
     if args.rows_only:
         print(json.dumps({"rows": _rows(args.steps)}), flush=True)
+        return 0
+    if args.configs_only:
+        print(json.dumps({"configs": _configs(args.steps)}), flush=True)
         return 0
 
     from eagle_harness.kernels.gdn_tree_conv import gdn_tree_conv1d_update
@@ -637,9 +893,16 @@ def main() -> int:
         "kernels": kernels,
         "cpu_baseline": _cpu_baseline(work, args.cpu_sample, args.cpu_seconds) if work is not None else None,
     }
+    print(f"[bench] step {wall / args.steps * 1e3:.3f} ms", file=sys.stderr, flush=True)
     if not args.step_only:
         result["records_chunk"] = _records_chunk(args.steps)
+        print("[bench] records chunk timed", file=sys.stderr, flush=True)
         result["rows"] = _rows(args.steps)
+        print("[bench] rows timed", file=sys.stderr, flush=True)
+        result["configs"] = _configs(args.steps)
+        print("[bench] configuration rounds timed", file=sys.stderr, flush=True)
+        if args.cpu_configs > 0:
+            result["cpu_configs"] = _cpu_configs(args.cpu_configs)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -2,25 +2,29 @@
 //
 // HBM-bound: per request it reads the nodes' inputs, the history columns of the conv state and the weights once,
 // and writes the outputs, the windows and the rolled state once. One workgroup takes one request and a block of
-// kChannels channels. It stages the block's node inputs (token-major, 16 bytes per 8 channels), the ancestor codes,
-// the weights and the history in LDS; every thread then computes the outputs of its 8 channels for a strided set of
-// nodes, each window gathered from LDS through the ancestor table; the state roll is written after a barrier.
+// kChannels channels. It stages the block's node inputs (token-major, 16 bytes per 8 channels; LDS DMA when the rows
+// are 16-byte vectors), the ancestor codes, the weights and the history in LDS; every thread then computes the outputs
+// of its 8 channels for a strided set of nodes, each window gathered from LDS through the ancestor table, and writes
+// its part of the state roll.
 //
 // When the state rows are contiguous (token stride 1, channel stride = state length: the block's rows are one
-// 16-byte-aligned span) the whole span is copied into LDS, rolled there and written back with 16-byte stores, so no
-// cache line is left partly written; otherwise the roll is written element by element along the contiguous
-// dimension. LDS is sized at launch for the widest tree and the state length.
+// 16-byte-aligned span of kChannels * L elements) each thread loads its 16-byte pieces of the span into registers at
+// the start, hands the history columns it holds to LDS, and after the barrier writes the rolled pieces back with
+// 16-byte stores, so no cache line is left partly written and the span is read once; otherwise the history is read
+// element by element and the roll written element by element along the contiguous dimension.
 
 #include "common.h"
 
 namespace {
 
-constexpr int kChannels = 128;          // channels per workgroup
+constexpr int kChannels = 256;          // channels per workgroup
 constexpr int kVecs = kChannels / 8;    // 8-channel vectors per node
 constexpr int kThreads = 256;
 constexpr int kTokLanes = kThreads / kVecs;  // nodes computed concurrently
 constexpr int kMaxNodes = 64;
-constexpr int kMaxRowSpan = 96;         // state length of the LDS roll
+constexpr int kTokPerDma = 64 / kVecs;  // node inputs per 1 KB direct load
+static_assert(kVecs <= 64 && 64 % kVecs == 0, "a direct load covers whole node inputs");
+constexpr int kRowRegs = 5;             // at most 16-byte pieces of the state span per thread (rows of up to 40 columns)
 
 // One product of the upstream conv: 16-bit operands, product rounded (nearest even, v_cvt_pk_bf16_f32 /
 // v_cvt_f16_f32) to the 16-bit dtype, returned as fp32 (kernels/gdn_tree_conv.py:225-229, 429-430).
@@ -43,22 +47,24 @@ E4_DEV uint16_t lane16(const uint4& v, int i) {
   return static_cast<uint16_t>((i & 1) ? (w >> 16) : (w & 0xffffu));
 }
 
-// LDS layout (byte offsets): node inputs [seqlen][kVecs] x 16, state rows [kChannels][state_len] x 2 (row roll
-// only), history [3][kChannels] x 2, weights [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes [3][seqlen].
+// 64 lanes x 16 bytes from per-lane global addresses into LDS [dst, dst + 1024), lane p at dst + 16 p.
+E4_DEV void dma16(const void* src, char* dst) { __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0); }
+
+// LDS layout (byte offsets): node inputs [seqlen rounded up to kTokPerDma][kVecs] x 16, history [3][kChannels] x 2, weights
+// [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes [3][seqlen].
 struct Lds {
-  int xs, rows, hist, wts, bias, anc, total;
-  int row_roll;
+  int xs, hist, wts, bias, anc, total;
+  int row_roll;  // the state span is held in registers and written back whole
 };
 
 Lds lds_layout(const eagle4_conv_args& a) {
   auto up16 = [](int b) { return (b + 15) / 16 * 16; };
   Lds l;
-  l.row_roll = a.stride_cs_tok == 1 && a.stride_cs_dim == a.state_len && a.state_len <= kMaxRowSpan &&
-               a.dim % kChannels == 0 && (reinterpret_cast<uintptr_t>(a.conv_state) & 15) == 0 &&
-               (a.stride_cs_seq * 2) % 16 == 0;
+  l.row_roll = a.stride_cs_tok == 1 && a.stride_cs_dim == a.state_len &&
+               kChannels * a.state_len / 8 <= kRowRegs * kThreads && a.dim % kChannels == 0 &&
+               (reinterpret_cast<uintptr_t>(a.conv_state) & 15) == 0 && (a.stride_cs_seq * 2) % 16 == 0;
   l.xs = 0;
-  l.rows = up16(a.seqlen * kVecs * 16);
-  l.hist = l.rows + (l.row_roll ? up16(kChannels * a.state_len * 2) : 0);
+  l.hist = up16((a.seqlen + kTokPerDma - 1) / kTokPerDma * 1024);
   l.wts = l.hist + up16(3 * kChannels * 2);
   l.bias = l.wts + up16(4 * kChannels * 2);
   l.anc = l.bias + kChannels * 4;
@@ -66,19 +72,18 @@ Lds lds_layout(const eagle4_conv_args& a) {
   return l;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
+// R: the span pieces a thread holds (row roll; any value otherwise)
+template <typename T, int R>
+__global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint4* const xs = reinterpret_cast<uint4*>(lds + off.xs);        // [t * kVecs + v]
-  uint16_t* const rows = reinterpret_cast<uint16_t*>(lds + off.rows);  // [c * state_len + col]
   uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c]
   uint16_t* const wts = reinterpret_cast<uint16_t*>(lds + off.wts);    // [j * kChannels + c]
   float* const bias_s = reinterpret_cast<float*>(lds + off.bias);
   int* const anc = reinterpret_cast<int*>(lds + off.anc);             // [j * n + t]
   const int seq = blockIdx.y;
   const int cb = blockIdx.x * kChannels;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int L = a.state_len;
 
   // _conv_request (:43-56)
@@ -101,22 +106,33 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
   uint16_t* state = static_cast<uint16_t*>(a.conv_state) + slot * a.stride_cs_seq +
                     static_cast<int64_t>(cb) * a.stride_cs_dim;
 
-  // ---- stage: node inputs, ancestor codes, weights, bias, state ---------------------------------------------------
+  // ---- stage: the state span (registers), node inputs, ancestor codes, weights, bias, history --------------------
+  const int span = kChannels * L / 8;  // 16-byte pieces of the block's state rows (row roll)
+  uint4 rows[R];
+  if (off.row_roll) {
+    const uint4* src = reinterpret_cast<const uint4*>(state);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = tid + r * kThreads;
+      if (i < span) rows[r] = src[i];
+    }
+  }
   const bool xvec = a.stride_x_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                     ((a.stride_x_token | a.stride_x_seq | cb) & 7) == 0;
-  for (int i = tid; i < n * kVecs; i += kThreads) {
-    const int t = i / kVecs, v = i % kVecs;
-    const uint16_t* p = x + t * a.stride_x_token + 8 * v * a.stride_x_dim;
-    uint4 r;
-    if (xvec) {
-      r = *reinterpret_cast<const uint4*>(p);
-    } else {
+  if (xvec) {  // instruction m fills tokens kTokPerDma m .. + kTokPerDma - 1 (past the last token: the last again)
+    for (int m = wave; kTokPerDma * m < n; m += kThreads / 64) {
+      const int t0 = kTokPerDma * m + lane / kVecs, t = t0 < n ? t0 : n - 1;
+      dma16(x + t * a.stride_x_token + 8 * (lane % kVecs), lds + off.xs + m * 1024);
+    }
+  } else {
+    for (int i = tid; i < n * kVecs; i += kThreads) {
+      const int t = i / kVecs, v = i % kVecs;
+      const uint16_t* p = x + t * a.stride_x_token + 8 * v * a.stride_x_dim;
       uint32_t h[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) h[e] = 8 * v + e < nch ? p[e * a.stride_x_dim] : 0u;
-      r = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+      xs[i] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
     }
-    xs[i] = r;
   }
   const int32_t* atab = a.ancestors + static_cast<int64_t>(seq) * 3 * a.seqlen;
   for (int i = tid; i < 3 * n; i += kThreads) anc[i] = atab[(i / n) * a.seqlen + i % n];
@@ -131,24 +147,30 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
       bias_s[c] = (c < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c, a.bias_dtype) : 0.f;
   }
   const bool tok_fast = a.stride_cs_tok == 1;  // lanes along the state's contiguous dimension
-  if (off.row_roll) {
-    const uint4* src = reinterpret_cast<const uint4*>(state);
-    uint4* dst = reinterpret_cast<uint4*>(rows);
-    for (int i = tid; i < kChannels * L / 8; i += kThreads) dst[i] = src[i];
+  if (off.row_roll) {  // the history columns out of this thread's pieces of the span
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = tid + r * kThreads;
+      if (i >= span) break;
+      int c = (8 * i) / L, col = 8 * i - c * L;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = col - static_cast<int>(history);
+        if (j >= 0 && j < 3) hist[j * kChannels + c] = lane16(rows[r], e);
+        if (++col == L) {
+          col = 0;
+          ++c;
+        }
+      }
+    }
   } else {
     for (int i = tid; i < 3 * kChannels; i += kThreads) {
       const int c = tok_fast ? i / 3 : i % kChannels, j = tok_fast ? i % 3 : i / kChannels;
       hist[j * kChannels + c] = c < nch ? state[c * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : 0;
     }
   }
+  if (xvec) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct loads have landed in LDS
   __syncthreads();
-  if (off.row_roll) {  // the history columns out of the staged rows, before the roll rewrites them
-    for (int i = tid; i < 3 * kChannels; i += kThreads) {
-      const int c = i / 3, j = i % 3;
-      hist[j * kChannels + c] = rows[c * L + history + j];
-    }
-    __syncthreads();
-  }
 
   // ---- outputs: thread (token lane tl, vector v) computes channels 8 v .. 8 v + 7 of nodes tl, tl + kTokLanes, ... ---
   {
@@ -213,22 +235,23 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
   }
 
   // ---- the roll (:266-278): history column j goes to column j + shift, node t's input to t + 3 + shift (kept when
-  // the column is >= 0); every history read was staged before the first barrier -----------------------------------
+  // the column is >= 0); every history read was staged before the barrier --------------------------------------------
   const int shift = static_cast<int>((num_tokens + 2 < L ? num_tokens + 2 : L) - num_tokens - 3);
   const int cols = 3 + n;  // source columns: history 0..2, then the nodes
   if (off.row_roll) {
-    // the block's rows assembled 8 elements at a time: column col of channel c takes source col - shift when that is
-    // a source column, and keeps its staged value otherwise
-    const uint4* old = reinterpret_cast<const uint4*>(rows);
+    // this thread's pieces of the span, 8 elements each: column col of channel c takes source col - shift when that
+    // is a source column, and keeps its loaded value otherwise
     uint4* dst = reinterpret_cast<uint4*>(state);
-    for (int i = tid; i < kChannels * L / 8; i += kThreads) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int i = tid + r * kThreads;
+      if (i >= span) break;
       int c = (8 * i) / L, col = 8 * i - c * L;
-      const uint4 o = old[i];
       uint32_t w[4];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int src = col - shift;
-        uint16_t val = lane16(o, e);
+        uint16_t val = lane16(rows[r], e);
         if (src >= 0 && src < cols)
           val = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
         w[e / 2] = (e & 1) ? (w[e / 2] | static_cast<uint32_t>(val) << 16) : val;
@@ -261,9 +284,16 @@ extern "C" int eagle4_gdn_tree_conv1d_update(const eagle4_conv_args* a, void* st
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const Lds off = lds_layout(*a);
   const dim3 grid(e4::ceil_div(a->dim, kChannels), a->batch);
-  if (a->dtype == EAGLE4_BF16)
-    tree_conv_kernel<e4::Bf16><<<grid, kThreads, off.total, s>>>(*a, off);
+  const int regs = off.row_roll ? e4::ceil_div(kChannels * a->state_len / 8, kThreads) : 1;
+  auto launch = [&](auto kernel) { kernel<<<grid, kThreads, off.total, s>>>(*a, off); };
+  const bool bf = a->dtype == EAGLE4_BF16;
+  if (regs <= 1)
+    bf ? launch(tree_conv_kernel<e4::Bf16, 1>) : launch(tree_conv_kernel<e4::F16, 1>);
+  else if (regs <= 2)
+    bf ? launch(tree_conv_kernel<e4::Bf16, 2>) : launch(tree_conv_kernel<e4::F16, 2>);
+  else if (regs <= 3)
+    bf ? launch(tree_conv_kernel<e4::Bf16, 3>) : launch(tree_conv_kernel<e4::F16, 3>);
   else
-    tree_conv_kernel<e4::F16><<<grid, kThreads, off.total, s>>>(*a, off);
+    bf ? launch(tree_conv_kernel<e4::Bf16, kRowRegs>) : launch(tree_conv_kernel<e4::F16, kRowRegs>);
   return E4_LAUNCH_STATUS();
 }

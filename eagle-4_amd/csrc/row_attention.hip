@@ -91,7 +91,7 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
   // hides behind a tile, and the tile's K / V load one tile ahead into the other LDS buffer.
   constexpr int RPI = TL::RPI, NI = TL::NI, NIW = NI / NW;
   static_assert(NI % NW == 0, "instructions per wave");
-  uint32_t raw[NIW], rem[NIW];  // page-table entry (or ancestor slot) and position within the page (or validity)
+  uint32_t raw[NIW], rem[NIW];  // page-table entry and position within the page (or the ancestor's KV slot)
   auto lookup = [&](int tile) {
     const int64_t base = start + static_cast<int64_t>(tile) * kTileKeys;
 #pragma unroll
@@ -100,10 +100,12 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
       const int64_t c = base + row < end ? base + row : end - 1;  // past the split: its last key (masked later)
       if (anc) {
         const int owner = static_cast<int>(c / a.max_depth), dep = static_cast<int>(c % a.max_depth);
-        const bool valid = dep < a.step;  // owner < rows_per_request: the split ends at rows * max_depth
+        // owner < rows_per_request: the split ends at rows * max_depth. A column past the row's `step` ancestors
+        // loads the row's first ancestor instead (written: the split exists only for step >= 1), so the masked key
+        // multiplies finite data, never a slot nobody wrote
+        const bool valid = dep < a.step;
         raw[i] = static_cast<uint32_t>(
             a.ancestors[(static_cast<int64_t>(b) * a.rows_per_request + owner) * a.max_depth + (valid ? dep : 0)]);
-        rem[i] = valid;
       } else {
         const uint32_t pos = static_cast<uint32_t>(c), tp = static_cast<uint32_t>(a.table_page);
         const uint32_t pg = tp_shift >= 0 ? pos >> tp_shift : pos / tp;
@@ -118,7 +120,7 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
 #pragma unroll
     for (int i = 0; i < NIW; ++i) {
       const int n = wave + NW * i, row = n * RPI + lane / CH, pc = lane % CH;
-      const uint32_t slot = anc ? (rem[i] ? raw[i] : 0u) : raw[i] * static_cast<uint32_t>(a.table_page) + rem[i];
+      const uint32_t slot = anc ? raw[i] : raw[i] * static_cast<uint32_t>(a.table_page) + rem[i];
       const uint32_t cpg = static_cast<uint32_t>(a.cache_page);
       const uint32_t blk = cp_shift >= 0 ? slot >> cp_shift : slot / cpg, in = slot - blk * cpg;
       const int64_t koff = 2 * (blk * a.k_stride_page + in * a.k_stride_slot + kvh * a.k_stride_head);

@@ -107,14 +107,22 @@ def test_accept_tail_matches_oracle(dev, seed):
 
 
 @pytest.mark.parametrize("ssm_dtype", [torch.float32, torch.bfloat16])
-def test_linear_state_commit_matches_oracle(dev, ssm_dtype):
+@pytest.mark.parametrize("layout,conv_dtype,dim", [("rows", torch.bfloat16, 40), ("rows", torch.bfloat16, 600),
+                                                   ("rows", torch.float32, 300), ("columns", torch.bfloat16, 600)])
+def test_linear_state_commit_matches_oracle(dev, ssm_dtype, layout, conv_dtype, dim):
+    """Window caches with contiguous rows (moved as whole 16-byte pieces; rows of 10 elements, so pieces straddle
+    channels; blocks of 256 / 128 channels and a partial last block) and column-major ones (moved element-wise)."""
     from eagle_harness.vllm.gdn_tree_verify import LinearStateCommit
 
-    announce(f"state commit {ssm_dtype}")
+    announce(f"state commit {ssm_dtype} {layout} {conv_dtype} dim {dim}")
     gen = torch.Generator().manual_seed(4)
-    layers, reqs, width, dim, hv, d = 2, 3, 8, 40, 2, 16
+    layers, reqs, width, hv, d = 2, 3, 8, 2, 16
     slots_n = 1 + reqs * width
-    convs = [torch.randn(slots_n, dim, 2 + width, generator=gen).to(torch.bfloat16) for _ in range(layers)]
+    if layout == "rows":
+        convs = [torch.randn(slots_n, dim, 2 + width, generator=gen).to(conv_dtype) for _ in range(layers)]
+    else:
+        convs = [torch.randn(slots_n, 2 + width, dim, generator=gen).to(conv_dtype).transpose(1, 2)
+                 for _ in range(layers)]
     ssms = [torch.randn(slots_n, hv, d, d, generator=gen).to(ssm_dtype) for _ in range(layers)]
     slots = (1 + torch.arange(reqs * width, dtype=torch.int32)).view(reqs, width)
     slots[2] = 0  # a padded request

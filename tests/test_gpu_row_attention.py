@@ -108,3 +108,26 @@ def test_gqa_packed_paged_cache(dev, step, D, dtype):
     anc = torch.randint(0, nslots, (bs, rows, 6), dtype=torch.int32, device=dev, generator=gen) if step else None
     got = _run(dev, q, cache, None, table, seq, anc, rows=rows, step=step, window=512, splits=32, table_page=tpage)
     _check(got, q, cache, None, table, seq, anc, rows_per_request=rows, step=step, window=512, table_page=tpage)
+
+
+@pytest.mark.parametrize("step", [1, 4])
+def test_masked_ancestor_columns_read_no_unwritten_slot(dev, step):
+    """A draft step's ancestor split has max_depth columns per row, of which the first ``step`` are the row's
+    ancestors; the masked columns past them must not read a slot nobody wrote. KV slot 0 holds NaN (as a null block
+    of a cache that is not zero-filled would) and no window key or ancestor uses it: the outputs stay finite and equal
+    the oracle's."""
+    announce(f"row attention masked ancestors with a NaN slot 0, step={step}")
+    bs, rows, depth, heads, D = 2, 4, 12, 3, 128
+    gen = torch.Generator(device=dev).manual_seed(77 + step)
+    nslots = 8 * 4096
+    table = (torch.randperm(nslots - 8, device=dev, generator=gen) + 8).to(torch.int32).view(8, 4095)
+    req = torch.tensor([5, 2], dtype=torch.int64, device=dev)
+    seq = torch.randint(40, 300, (bs,), device=dev, generator=gen)
+    k = torch.randn(nslots, heads, D, device=dev, generator=gen).bfloat16()
+    v = torch.randn(nslots, heads, D, device=dev, generator=gen).bfloat16()
+    k[0], v[0] = float("nan"), float("nan")
+    q = torch.randn(bs * rows, heads, D, device=dev, generator=gen).bfloat16()
+    anc = torch.randint(1, nslots, (bs, rows, depth), dtype=torch.int32, device=dev, generator=gen)
+    got = _run(dev, q, k, v, table, seq, anc, rows=rows, step=step, window=96, splits=8, table_rows=req)
+    assert torch.isfinite(got.float()).all()
+    _check(got, q, k, v, table, seq, anc, rows_per_request=rows, step=step, window=96, table_rows=req)
