@@ -1,17 +1,18 @@
 // Width-4 tree causal conv1d of a GDN verify on gfx950 (kernels/gdn_tree_conv.py:402-497).
 //
-// HBM-bound: per request it reads the nodes' inputs, the history columns of the conv state and the weights once,
-// and writes the outputs, the windows and the rolled state once. One workgroup takes one request and a block of
-// kChannels channels. It stages the block's node inputs (token-major, 16 bytes per 8 channels; LDS DMA when the rows
-// are 16-byte vectors), the ancestor codes, the weights and the history in LDS; every thread then computes the outputs
-// of its 8 channels for a strided set of nodes, each window gathered from LDS through the ancestor table, and writes
-// its part of the state roll.
+// Per request it reads the nodes' inputs, the history columns of the conv state and the weights once, and writes the
+// outputs, the windows and the rolled state once. One workgroup takes one request and a block of kChannels channels
+// (a thread per channel for the roll, an 8-channel octet per thread and node for the outputs). It stages the block's
+// node inputs (token-major, 16 bytes per 8 channels, LDS DMA when the rows are 16-byte vectors), the ancestor codes,
+// the weights and the history in LDS; every thread then computes the outputs of its octet for a strided set of
+// nodes, each window gathered from LDS through the ancestor table, and the roll follows.
 //
 // When the state rows are contiguous (token stride 1, channel stride = state length: the block's rows are one
-// 16-byte-aligned span of kChannels * L elements) each thread loads its 16-byte pieces of the span into registers at
-// the start, hands the history columns it holds to LDS, and after the barrier writes the rolled pieces back with
-// 16-byte stores, so no cache line is left partly written and the span is read once; otherwise the history is read
-// element by element and the roll written element by element along the contiguous dimension.
+// 16-byte-aligned span of kChannels * L elements) the span is copied into LDS by direct loads, each thread reads its
+// channel's history columns and later writes its channel's rolled row back into the copy (the loop over columns is
+// the same for every thread: no divergence), and the span leaves with 16-byte stores, so no cache line is left partly
+// written and the span is read once. Otherwise the history is read element by element and the roll written element
+// by element along the contiguous dimension.
 
 #include "common.h"
 
@@ -24,7 +25,9 @@ constexpr int kTokLanes = kThreads / kVecs;  // nodes computed concurrently
 constexpr int kMaxNodes = 64;
 constexpr int kTokPerDma = 64 / kVecs;  // node inputs per 1 KB direct load
 static_assert(kVecs <= 64 && 64 % kVecs == 0, "a direct load covers whole node inputs");
-constexpr int kRowRegs = 5;             // at most 16-byte pieces of the state span per thread (rows of up to 40 columns)
+static_assert(kThreads == kChannels, "a thread per channel for the roll");
+constexpr int kMaxSpan = 24 * 1024;    // bytes of a block's state rows staged for the roll (rows up to 48 columns),
+                                        // so the LDS stays within the 64 KB a launch gets without attributes
 
 // One product of the upstream conv: 16-bit operands, product rounded (nearest even, v_cvt_pk_bf16_f32 /
 // v_cvt_f16_f32) to the 16-bit dtype, returned as fp32 (kernels/gdn_tree_conv.py:225-229, 429-430).
@@ -50,21 +53,23 @@ E4_DEV uint16_t lane16(const uint4& v, int i) {
 // 64 lanes x 16 bytes from per-lane global addresses into LDS [dst, dst + 1024), lane p at dst + 16 p.
 E4_DEV void dma16(const void* src, char* dst) { __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0); }
 
-// LDS layout (byte offsets): node inputs [seqlen rounded up to kTokPerDma][kVecs] x 16, history [3][kChannels] x 2, weights
-// [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes [3][seqlen].
+// LDS layout (byte offsets): node inputs [seqlen rounded up to kTokPerDma][kVecs] x 16, the state span [kChannels][L]
+// x 2 (row roll), history [3][kChannels] x 2, weights [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes
+// [3][seqlen].
 struct Lds {
-  int xs, hist, wts, bias, anc, total;
-  int row_roll;  // the state span is held in registers and written back whole
+  int xs, rows, hist, wts, bias, anc, total;
+  int row_roll;  // the state span is staged in LDS and written back whole
 };
 
 Lds lds_layout(const eagle4_conv_args& a) {
   auto up16 = [](int b) { return (b + 15) / 16 * 16; };
   Lds l;
-  l.row_roll = a.stride_cs_tok == 1 && a.stride_cs_dim == a.state_len &&
-               kChannels * a.state_len / 8 <= kRowRegs * kThreads && a.dim % kChannels == 0 &&
-               (reinterpret_cast<uintptr_t>(a.conv_state) & 15) == 0 && (a.stride_cs_seq * 2) % 16 == 0;
+  l.row_roll = a.stride_cs_tok == 1 && a.stride_cs_dim == a.state_len && kChannels * a.state_len * 2 <= kMaxSpan &&
+               a.dim % kChannels == 0 && (reinterpret_cast<uintptr_t>(a.conv_state) & 15) == 0 &&
+               (a.stride_cs_seq * 2) % 16 == 0;
   l.xs = 0;
-  l.hist = up16((a.seqlen + kTokPerDma - 1) / kTokPerDma * 1024);
+  l.rows = (a.seqlen + kTokPerDma - 1) / kTokPerDma * 1024;
+  l.hist = l.rows + (l.row_roll ? (kChannels * a.state_len * 2 + 1023) / 1024 * 1024 : 0);
   l.wts = l.hist + up16(3 * kChannels * 2);
   l.bias = l.wts + up16(4 * kChannels * 2);
   l.anc = l.bias + kChannels * 4;
@@ -72,11 +77,11 @@ Lds lds_layout(const eagle4_conv_args& a) {
   return l;
 }
 
-// R: the span pieces a thread holds (row roll; any value otherwise)
-template <typename T, int R>
+template <typename T>
 __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint4* const xs = reinterpret_cast<uint4*>(lds + off.xs);        // [t * kVecs + v]
+  uint16_t* const rows = reinterpret_cast<uint16_t*>(lds + off.rows);  // [c * L + col] (row roll)
   uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c]
   uint16_t* const wts = reinterpret_cast<uint16_t*>(lds + off.wts);    // [j * kChannels + c]
   float* const bias_s = reinterpret_cast<float*>(lds + off.bias);
@@ -106,15 +111,12 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
   uint16_t* state = static_cast<uint16_t*>(a.conv_state) + slot * a.stride_cs_seq +
                     static_cast<int64_t>(cb) * a.stride_cs_dim;
 
-  // ---- stage: the state span (registers), node inputs, ancestor codes, weights, bias, history --------------------
+  // ---- stage: the state span, node inputs, ancestor codes, weights, bias ------------------------------------------
   const int span = kChannels * L / 8;  // 16-byte pieces of the block's state rows (row roll)
-  uint4 rows[R];
-  if (off.row_roll) {
-    const uint4* src = reinterpret_cast<const uint4*>(state);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = tid + r * kThreads;
-      if (i < span) rows[r] = src[i];
+  if (off.row_roll) {  // instruction k fills pieces 64 k .. 64 k + 63 (past the span: its last piece again)
+    for (int k = wave; 64 * k < span; k += kThreads / 64) {
+      const int i = 64 * k + lane < span ? 64 * k + lane : span - 1;
+      dma16(reinterpret_cast<const char*>(state) + 16 * i, lds + off.rows + k * 1024);
     }
   }
   const bool xvec = a.stride_x_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
@@ -147,29 +149,19 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
       bias_s[c] = (c < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c, a.bias_dtype) : 0.f;
   }
   const bool tok_fast = a.stride_cs_tok == 1;  // lanes along the state's contiguous dimension
-  if (off.row_roll) {  // the history columns out of this thread's pieces of the span
+  if (off.row_roll) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the span's direct loads have landed
+    __syncthreads();
+    const int c = tid;  // this thread's channel: its history columns out of the staged span
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = tid + r * kThreads;
-      if (i >= span) break;
-      int c = (8 * i) / L, col = 8 * i - c * L;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int j = col - static_cast<int>(history);
-        if (j >= 0 && j < 3) hist[j * kChannels + c] = lane16(rows[r], e);
-        if (++col == L) {
-          col = 0;
-          ++c;
-        }
-      }
-    }
+    for (int j = 0; j < 3; ++j) hist[j * kChannels + c] = rows[c * L + history + j];
   } else {
     for (int i = tid; i < 3 * kChannels; i += kThreads) {
       const int c = tok_fast ? i / 3 : i % kChannels, j = tok_fast ? i % 3 : i / kChannels;
       hist[j * kChannels + c] = c < nch ? state[c * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : 0;
     }
   }
-  if (xvec) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct loads have landed in LDS
+  if (xvec) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the nodes' direct loads have landed
   __syncthreads();
 
   // ---- outputs: thread (token lane tl, vector v) computes channels 8 v .. 8 v + 7 of nodes tl, tl + kTokLanes, ... ---
@@ -182,12 +174,13 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
     if (a.window != nullptr)
       window = static_cast<uint16_t*>(a.window) + e4::ld(a.window_indices, seq) * a.stride_win_seq +
                static_cast<int64_t>(cb + c0) * a.stride_win_dim;
-    uint4 wv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wv[j] = *reinterpret_cast<const uint4*>(&wts[j * kChannels + c0]);
-    const float4 b0 = *reinterpret_cast<const float4*>(&bias_s[c0]), b1 = *reinterpret_cast<const float4*>(&bias_s[c0 + 4]);
-    const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
     for (int t = tl; t < n; t += kTokLanes) {
+      uint4 wv[4];  // the taps, read per node: fewer registers held over the loop
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[j] = *reinterpret_cast<const uint4*>(&wts[j * kChannels + c0]);
+      const float4 b0 = *reinterpret_cast<const float4*>(&bias_s[c0]);
+      const float4 b1 = *reinterpret_cast<const float4*>(&bias_s[c0 + 4]);
+      const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       const uint4 xt = xs[t * kVecs + v];
       uint4 win[3];  // parent, grandparent, great-grandparent
 #pragma unroll
@@ -239,29 +232,17 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
   const int shift = static_cast<int>((num_tokens + 2 < L ? num_tokens + 2 : L) - num_tokens - 3);
   const int cols = 3 + n;  // source columns: history 0..2, then the nodes
   if (off.row_roll) {
-    // this thread's pieces of the span, 8 elements each: column col of channel c takes source col - shift when that
-    // is a source column, and keeps its loaded value otherwise
-    uint4* dst = reinterpret_cast<uint4*>(state);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int i = tid + r * kThreads;
-      if (i >= span) break;
-      int c = (8 * i) / L, col = 8 * i - c * L;
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int src = col - shift;
-        uint16_t val = lane16(rows[r], e);
-        if (src >= 0 && src < cols)
-          val = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
-        w[e / 2] = (e & 1) ? (w[e / 2] | static_cast<uint32_t>(val) << 16) : val;
-        if (++col == L) {
-          col = 0;
-          ++c;
-        }
-      }
-      dst[i] = make_uint4(w[0], w[1], w[2], w[3]);
+    // this thread's channel: the destination columns in order (the same loop in every thread), into the staged span
+    const int c = tid;
+    const int lo = shift > 0 ? shift : 0, hi = cols + shift < L ? cols + shift : L;
+    for (int col = lo; col < hi; ++col) {
+      const int src = col - shift;
+      rows[c * L + col] = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
     }
+    __syncthreads();
+    const uint4* staged = reinterpret_cast<const uint4*>(rows);
+    uint4* dst = reinterpret_cast<uint4*>(state);
+    for (int i = tid; i < span; i += kThreads) dst[i] = staged[i];
   } else {
     for (int i = tid; i < cols * kChannels; i += kThreads) {
       const int c = tok_fast ? i / cols : i % kChannels, src = tok_fast ? i % cols : i / kChannels;
@@ -284,16 +265,9 @@ extern "C" int eagle4_gdn_tree_conv1d_update(const eagle4_conv_args* a, void* st
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const Lds off = lds_layout(*a);
   const dim3 grid(e4::ceil_div(a->dim, kChannels), a->batch);
-  const int regs = off.row_roll ? e4::ceil_div(kChannels * a->state_len / 8, kThreads) : 1;
-  auto launch = [&](auto kernel) { kernel<<<grid, kThreads, off.total, s>>>(*a, off); };
-  const bool bf = a->dtype == EAGLE4_BF16;
-  if (regs <= 1)
-    bf ? launch(tree_conv_kernel<e4::Bf16, 1>) : launch(tree_conv_kernel<e4::F16, 1>);
-  else if (regs <= 2)
-    bf ? launch(tree_conv_kernel<e4::Bf16, 2>) : launch(tree_conv_kernel<e4::F16, 2>);
-  else if (regs <= 3)
-    bf ? launch(tree_conv_kernel<e4::Bf16, 3>) : launch(tree_conv_kernel<e4::F16, 3>);
+  if (a->dtype == EAGLE4_BF16)
+    tree_conv_kernel<e4::Bf16><<<grid, kThreads, off.total, s>>>(*a, off);
   else
-    bf ? launch(tree_conv_kernel<e4::Bf16, kRowRegs>) : launch(tree_conv_kernel<e4::F16, kRowRegs>);
+    tree_conv_kernel<e4::F16><<<grid, kThreads, off.total, s>>>(*a, off);
   return E4_LAUNCH_STATUS();
 }
