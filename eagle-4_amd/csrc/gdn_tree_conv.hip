@@ -29,15 +29,19 @@ static_assert(kThreads == kChannels, "a thread per channel for the roll");
 constexpr int kMaxSpan = 24 * 1024;    // bytes of a block's state rows staged for the roll (rows up to 48 columns),
                                         // so the LDS stays within the 64 KB a launch gets without attributes
 
-// One product of the upstream conv: 16-bit operands, product rounded (nearest even, v_cvt_pk_bf16_f32 /
-// v_cvt_f16_f32) to the 16-bit dtype, returned as fp32 (kernels/gdn_tree_conv.py:225-229, 429-430).
+// Two products of the upstream conv: 16-bit operands, each product rounded to nearest even in the 16-bit dtype and
+// returned as fp32 (kernels/gdn_tree_conv.py:225-229, 429-430); for bf16 one v_cvt_pk_bf16_f32 rounds both.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <typename T>
-E4_DEV float product(uint16_t x, uint16_t w) {
-  const float p = T::to_f32(x) * T::to_f32(w);
-  if constexpr (T::code == EAGLE4_BF16)
-    return static_cast<float>(static_cast<__bf16>(p));
-  else
-    return static_cast<float>(static_cast<_Float16>(p));
+E4_DEV f32x2 product2(uint16_t x0, uint16_t x1, float w0, float w1) {
+  const f32x2 p = {T::to_f32(x0) * w0, T::to_f32(x1) * w1};
+  if constexpr (T::code == EAGLE4_BF16) {
+    uint32_t r;  // both rounded by one instruction (the compiler splits a vector conversion here)
+    asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(p.x), "v"(p.y));
+    return f32x2{__uint_as_float(r << 16), __uint_as_float(r & 0xffff0000u)};
+  } else {
+    return f32x2{static_cast<float>(static_cast<_Float16>(p.x)), static_cast<float>(static_cast<_Float16>(p.y))};
+  }
 }
 
 // x sigmoid(x) = x / (1 + e^-x), e^-x as 2^(-x log2 e) on v_exp_f32 and the quotient on v_rcp_f32.
@@ -55,7 +59,7 @@ E4_DEV void dma16(const void* src, char* dst) { __builtin_amdgcn_global_load_lds
 
 // LDS layout (byte offsets): node inputs [seqlen rounded up to kTokPerDma][kVecs] x 16, the state span [kChannels][L]
 // x 2 (row roll), history [3][kChannels] x 2, weights [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes
-// [3][seqlen].
+// [3][seqlen]. The weights are held as fp32 (exact: they are 16-bit values).
 struct Lds {
   int xs, rows, hist, wts, bias, anc, total;
   int row_roll;  // the state span is staged in LDS and written back whole
@@ -71,7 +75,7 @@ Lds lds_layout(const eagle4_conv_args& a) {
   l.rows = (a.seqlen + kTokPerDma - 1) / kTokPerDma * 1024;
   l.hist = l.rows + (l.row_roll ? (kChannels * a.state_len * 2 + 1023) / 1024 * 1024 : 0);
   l.wts = l.hist + up16(3 * kChannels * 2);
-  l.bias = l.wts + up16(4 * kChannels * 2);
+  l.bias = l.wts + up16(4 * kChannels * 4);
   l.anc = l.bias + kChannels * 4;
   l.total = l.anc + up16(3 * a.seqlen * 4);
   return l;
@@ -83,7 +87,7 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
   uint4* const xs = reinterpret_cast<uint4*>(lds + off.xs);        // [t * kVecs + v]
   uint16_t* const rows = reinterpret_cast<uint16_t*>(lds + off.rows);  // [c * L + col] (row roll)
   uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c]
-  uint16_t* const wts = reinterpret_cast<uint16_t*>(lds + off.wts);    // [j * kChannels + c]
+  float* const wts = reinterpret_cast<float*>(lds + off.wts);          // [j * kChannels + c]
   float* const bias_s = reinterpret_cast<float*>(lds + off.bias);
   int* const anc = reinterpret_cast<int*>(lds + off.anc);             // [j * n + t]
   const int seq = blockIdx.y;
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
     const uint16_t* wsrc = static_cast<const uint16_t*>(a.weight) + static_cast<int64_t>(cb) * a.stride_w_dim;
     for (int i = tid; i < 4 * kChannels; i += kThreads) {
       const int c = tap_fast ? i / 4 : i % kChannels, j = tap_fast ? i % 4 : i / kChannels;
-      wts[j * kChannels + c] = c < nch ? wsrc[c * a.stride_w_dim + j * a.stride_w_width] : 0;
+      wts[j * kChannels + c] = c < nch ? T::to_f32(wsrc[c * a.stride_w_dim + j * a.stride_w_width]) : 0.f;
     }
     for (int c = tid; c < kChannels; c += kThreads)
       bias_s[c] = (c < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c, a.bias_dtype) : 0.f;
@@ -175,9 +179,15 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
       window = static_cast<uint16_t*>(a.window) + e4::ld(a.window_indices, seq) * a.stride_win_seq +
                static_cast<int64_t>(cb + c0) * a.stride_win_dim;
     for (int t = tl; t < n; t += kTokLanes) {
-      uint4 wv[4];  // the taps, read per node: fewer registers held over the loop
+      float wv[4][8];  // the taps, read per node: fewer registers held over the loop
 #pragma unroll
-      for (int j = 0; j < 4; ++j) wv[j] = *reinterpret_cast<const uint4*>(&wts[j * kChannels + c0]);
+      for (int j = 0; j < 4; ++j) {
+        const float4 w0 = *reinterpret_cast<const float4*>(&wts[j * kChannels + c0]);
+        const float4 w1 = *reinterpret_cast<const float4*>(&wts[j * kChannels + c0 + 4]);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wv[j][e] = w[e];
+      }
       const float4 b0 = *reinterpret_cast<const float4*>(&bias_s[c0]);
       const float4 b1 = *reinterpret_cast<const float4*>(&bias_s[c0 + 4]);
       const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
@@ -192,15 +202,20 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
+        // channels e, e + 1 together; per channel the sum in the reference's order: bias, then self w3, parent w2,
+        // grandparent w1, great-grandparent w0
+        const f32x2 p3 = product2<T>(lane16(xt, e), lane16(xt, e + 1), wv[3][e], wv[3][e + 1]);
+        const f32x2 p2 = product2<T>(lane16(win[0], e), lane16(win[0], e + 1), wv[2][e], wv[2][e + 1]);
+        const f32x2 p1 = product2<T>(lane16(win[1], e), lane16(win[1], e + 1), wv[1][e], wv[1][e + 1]);
+        const f32x2 p0 = product2<T>(lane16(win[2], e), lane16(win[2], e + 1), wv[0][e], wv[0][e + 1]);
         float r[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
           float acc = bias[e + k];
-          // self w3, parent w2, grandparent w1, great-grandparent w0
-          acc += product<T>(lane16(xt, e + k), lane16(wv[3], e + k));
-          acc += product<T>(lane16(win[0], e + k), lane16(wv[2], e + k));
-          acc += product<T>(lane16(win[1], e + k), lane16(wv[1], e + k));
-          acc += product<T>(lane16(win[2], e + k), lane16(wv[0], e + k));
+          acc += p3[k];
+          acc += p2[k];
+          acc += p1[k];
+          acc += p0[k];
           if (a.silu) acc = silu(acc);
           r[k] = acc;
         }
