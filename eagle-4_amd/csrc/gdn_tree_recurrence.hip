@@ -15,9 +15,12 @@
 // continues from registers instead; :318-329). Rows are parent first but otherwise in any order, so in index order
 // most parents are not the row just computed and ~3/4 of the nodes reload 64 KB each. Here a request whose reloads
 // are guaranteed to return the parent's own snapshot (parents precede children, every row has a real slot, no two
-// rows share one, at most 64 rows) is walked depth first instead (pre-order, children by index): a node's first
-// child continues from the registers, and a node with more children parks its state on a small per-wave LDS stack
-// that its later children pop (LIFO: when a later child of p comes, every state pushed after p has been popped).
+// rows share one, at most 64 rows) is walked depth first instead (pre-order): a node's first child continues from
+// the registers, and a node with more children parks its state on a small per-wave LDS stack that its later children
+// pop (LIFO: when a later child of p comes, every state pushed after p has been popped). A node's children are walked
+// in increasing order of the stack entries their subtrees need, the neediest last, so two entries cover every tree
+// whose nesting of multi-child nodes is at most two deep in that sense (all 16-node trees of up to 4 children per
+// node in these workloads; in index order such trees overflow two entries ~1.1 times per tree).
 // Parked states are what a reload would give (rounded through the snapshot dtype; exact in fp32), so the results
 // are bit-identical to the index-order walk. When the stack is full a node is not parked and its later children
 // reload its snapshot from HBM, as the reference does. Any other request keeps the reference's index-order walk
@@ -110,6 +113,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   int par = 0;
   int64_t my_slot = cache_idx;
   uint64_t kids = 0;
+  int first = -1, after = -1;  // lane u: u's first child in walk order; the sibling walked after u (-1: none)
   bool dfs = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
   if (dfs && lane < T) {
     par = static_cast<int>(e4::ld(a.parents, n, lane));
@@ -149,6 +153,36 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
         const uint64_t m = __ballot(lane > 0 && lane < T && par == i);
         if (lane == i) kids = m;
       }
+      // The order of the children. A node with several children holds a stack entry while its earlier children's
+      // subtrees are walked, so walking the child whose subtree needs the most entries last keeps the stack shallow:
+      // need(u) = 0 for a leaf, need(child) for one child, else max(largest, second largest + 1) over the children
+      // (Sethi-Ullman numbering). Children go in increasing (need, index); the values do not depend on the order. With
+      // 16-bit snapshots and the chain-child rule a chain child must be the first child (it continues unrounded from
+      // the registers), so that case keeps the index order.
+      int need = 0, m1 = 0, m2 = -1, nk = 0;  // lane u: u's need; the two largest needs among its children, their count
+      for (int i = T - 1; i >= 1; --i) {  // children before parents (rows are parent first)
+        const int nki = readlane(nk, i), m1i = readlane(m1, i), m2i = readlane(m2, i);
+        const int needi = nki == 0 ? 0 : (nki == 1 ? m1i : (m1i > m2i + 1 ? m1i : m2i + 1));
+        if (lane == i) need = needi;
+        if (lane == readlane(par, i)) {
+          ++nk;
+          if (needi > m1) {
+            m2 = m1;
+            m1 = needi;
+          } else if (needi > m2) {
+            m2 = needi;
+          }
+        }
+      }
+      const int key = (kExact || !a.skip_chain_reload ? need * 64 : 0) + lane;
+      int after_key = 1 << 30, first_key = 1 << 30;
+      for (int j = 1; j < T; ++j) {
+        const int kj = readlane(key, j), pj = readlane(par, j);
+        if (pj == par && kj > key && kj < after_key) after_key = kj;
+        if (pj == lane && kj < first_key) first_key = kj;
+      }
+      after = after_key == 1 << 30 ? -1 : (after_key & 63);
+      first = first_key == 1 << 30 ? -1 : (first_key & 63);
     }
   }
 
@@ -253,20 +287,18 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     int next = -1;
     bool next_first = false, next_last = false;
     if (dfs) {
-      const uint64_t ku = readlane64(kids, u);
-      if (ku != 0) {
-        next = __builtin_ctzll(ku);
+      const int fc = readlane(first, u);
+      if (fc >= 0) {
+        next = fc;
         next_first = true;
       } else {
-        for (int x = u; x != 0;) {
-          const int px = readlane(par, x);
-          const uint64_t sib = x == 63 ? 0 : readlane64(kids, px) & (~0ull << (x + 1));
-          if (sib != 0) {
-            next = __builtin_ctzll(sib);
-            next_last = (sib & (sib - 1)) == 0;
+        for (int x = u; x != 0; x = readlane(par, x)) {
+          const int sx = readlane(after, x);
+          if (sx >= 0) {
+            next = sx;
+            next_last = readlane(after, sx) < 0;
             break;
           }
-          x = px;
         }
       }
     } else if (u + 1 < T) {
