@@ -106,6 +106,7 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
         const bool valid = dep < a.step;
         raw[i] = static_cast<uint32_t>(
             a.ancestors[(static_cast<int64_t>(b) * a.rows_per_request + owner) * a.max_depth + (valid ? dep : 0)]);
+        rem[i] = 0;  // unused by the ancestor split; defined on both paths (left undefined, 12 registers spilled)
       } else {
         const uint32_t pos = static_cast<uint32_t>(c), tp = static_cast<uint32_t>(a.table_page);
         const uint32_t pg = tp_shift >= 0 ? pos >> tp_shift : pos / tp;
