@@ -50,12 +50,33 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build the gfx950 kernels)")
 
 
+def _spills(stderr: str) -> list[str]:
+    """Kernels whose resource-usage remarks report spilled vector registers or scratch memory, as "name: what".
+    (Scalar registers spill into vector-register lanes, not memory, and are left alone.)"""
+    found, name = [], None
+    for line in stderr.splitlines():
+        if "remark: Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[")[0].strip()
+        for key in ("VGPRs Spill:", "ScratchSize [bytes/lane]:"):
+            if key in line and name is not None:
+                value = int(line.split(key)[1].split("[")[0].strip())
+                if value > 0:
+                    found.append(f"{name}: {key} {value}")
+    return found
+
+
 def _compile(hipcc: str, src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-Rpass-analysis=kernel-resource-usage", "-c",
+           str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+    # a kernel that spills vector registers to scratch runs its inner loops through memory: refuse the build
+    spilled = _spills(proc.stderr)
+    if spilled:
+        raise RuntimeError(f"{src.name}: kernels spill vector registers (the hot loops would go through scratch):\n  "
+                           + "\n  ".join(spilled))
     return obj
 
 
