@@ -5,20 +5,41 @@
 // LPR = dstate / 16 lanes share a head-dim row m, each holding 16 fp32 state elements as four 4-element chunks
 // c = lane_in_row + LPR j (so a row's lanes write one contiguous run per store), a wave holds 64 / LPR rows and the
 // four waves 256 / LPR. Every node updates the state in registers (exp(A dt) decay, dt B x input), stores it to its
-// slot and reduces C . state over the row's lanes (xor shuffles). A node whose parent is the previous row continues
-// from the registers; any other reloads its parent's stored state (rounded through the pool dtype, as the reference
-// reads it); each lane reads back only elements it wrote itself, so no barrier is needed (:56-61 of the reference's
-// walk; it syncs because its load and store layouts differ across threads). The walk is store-bound: every node writes
+// slot and reduces C . state over the row's lanes (xor shuffles). The walk is store-bound: every node writes
 // head_dim x dstate state elements.
+//
+// Which state a node starts from. The reference walks the rows in index order; a row whose parent is the previous
+// row continues from the registers, any other reloads its parent's stored state (rounded through the pool dtype;
+// zeros for a pad slot). Here a request whose reloads are guaranteed to return the parent's own stored state (parents
+// precede children, every row has a real slot, no two rows share one, at most 64 rows) is walked depth first: a
+// node's first child continues from the registers (rounded through the pool dtype unless it is the chain child, as
+// the reference's reload would round it), and a node with more children parks its state, rounded as a reload would
+// give it, on a per-wave LDS stack of two entries that its later children pop. With an fp32 pool the children are
+// walked in increasing order of the stack entries their subtrees need (Sethi-Ullman numbering, the neediest last),
+// so two entries cover the trees; a 16-bit pool keeps the index order among children (its chain child, the lowest
+// index, must come first to continue unrounded). When the stack is full the later children reload from HBM as the
+// reference does. Any other request keeps the reference's index-order walk with its reloads (each lane reads back
+// only elements it wrote itself, so no barrier is needed; :56-61 of the reference's walk).
+//
+// No load waits behind stores: gfx950 counts loads and stores in one vmcnt, so a global load inside the node loop
+// would wait for the snapshot stores before it. The first TS nodes' B, C (fp32), x rows and (dt, exp(A dt)) are staged
+// in LDS before the walk; later nodes and the rare reloads settle their own loads.
 
-#include "common.h"
+#include "gdn_walk.h"
 
 namespace {
+
+using e4walk::readlane;
+using e4walk::readlane64;
+using e4walk::settle_loads;
+using e4walk::uni;
+using e4walk::uni64;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int NT = 256;
+constexpr int kStack = 2;  // parked states per wave
 
 template <typename S>
 E4_DEV f32x4 load4(const typename S::storage* p) {
@@ -42,73 +63,252 @@ E4_DEV void store4(typename S::storage* p, f32x4 v) {
   }
 }
 
+// four elements of B or C (in_dtype) as fp32
+E4_DEV f32x4 load_in4(const void* p, int64_t i, int dtype) {
+  if (dtype == EAGLE4_F32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  if (dtype == EAGLE4_BF16) return load4<e4::Bf16>(static_cast<const uint16_t*>(p) + i);
+  return load4<e4::F16>(static_cast<const uint16_t*>(p) + i);
+}
+
 // softplus as the reference writes it (:38-39): log(exp(dt) + 1) up to 20, dt above
 E4_DEV float softplus(float dt) { return dt <= 20.f ? logf(expf(dt) + 1.f) : dt; }
 
 template <int LPR, typename S>
 __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_args a) {
   using SS = typename S::storage;
-  constexpr int ROWS = NT / LPR;
+  constexpr int ROWS = NT / LPR;           // head-dim rows per workgroup
+  constexpr int DS = 16 * LPR;             // dstate
+  constexpr int TS = DS >= 256 ? 8 : 16;   // staged nodes
+  constexpr bool kExact = sizeof(SS) == 4; // fp32 pool: a reload gives the registers bit for bit
+  __shared__ __align__(16) f32x4 s_stack[NT / 64][kStack][4][64];
+  __shared__ __align__(16) float s_B[TS][DS];
+  __shared__ __align__(16) float s_C[TS][DS];
+  __shared__ float s_x[TS][ROWS];
+  __shared__ float2 s_g[TS];  // a staged node's (dt, exp(A dt))
+
   const int b = blockIdx.y, h = blockIdx.z;
-  const int lane = threadIdx.x & 63, lr = lane % LPR;
-  const int m = blockIdx.x * ROWS + (threadIdx.x >> 6) * (64 / LPR) + lane / LPR;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane % LPR;
+  const int row0 = blockIdx.x * ROWS;
+  const int lrow = wave * (64 / LPR) + lane / LPR;  // the lane's row within the workgroup
+  const int m = row0 + lrow;
   const bool mok = m < a.head_dim;
-  const int64_t bos = e4::ld(a.query_start_loc, b);
-  const int64_t seq = e4::ld(a.query_start_loc, b + 1) - bos;
-  if (seq <= 0) return;
+  const int64_t bos = uni64(e4::ld(a.query_start_loc, b));
+  const int T = static_cast<int>(uni64(e4::ld(a.query_start_loc, b + 1)) - bos);
+  if (T <= 0) return;
   const int g = h / (a.heads / a.groups);
   const int64_t pad = a.pad_slot_id;
-
   SS* const hstate = static_cast<SS*>(a.state) + h * a.stride_state_head + static_cast<int64_t>(m) * a.stride_state_dim;
-  f32x4 s[4];
-  auto load_slot = [&](int64_t slot) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = 4 * (lr + LPR * j);
-      s[j] = (slot != pad && mok) ? load4<S>(hstate + slot * a.stride_state_slot + n) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  const int64_t init_row = a.num_accepted.ptr != nullptr ? (e4::ld(a.num_accepted, b) - 1 > 0 ? e4::ld(a.num_accepted, b) - 1 : 0) : 0;
-  load_slot(e4::ld(a.slots, b, init_row));
-
   const float A = a.A[h];
   const float Dh = a.D != nullptr ? e4::load_scalar(a.D, h, a.param_dtype) : 0.f;
   const float dtb = a.dt_bias != nullptr ? e4::load_scalar(a.dt_bias, h, a.param_dtype) : 0.f;
-  for (int64_t t = 0; t < seq; ++t) {
-    const int64_t tok = bos + t;
-    const int64_t parent = e4::ld(a.parents, b, t);
-    if (t > 0 && parent != t - 1) load_slot(e4::ld(a.slots, b, parent));
-    const float x = mok ? e4::load_scalar(a.x, tok * a.stride_x_tok + h * a.stride_x_head + m, a.in_dtype) : 0.f;
-    float dt = e4::load_scalar(a.dt, tok * a.stride_dt_tok + h * a.stride_dt_head, a.dt_dtype) + dtb;
-    if (a.dt_softplus) dt = softplus(dt);
-    const float dA = exp2f(1.4426950408889634f * (A * dt));
-    const int64_t bo = tok * a.stride_B_tok + g * a.stride_B_group, co = tok * a.stride_C_tok + g * a.stride_C_group;
-    float part = 0.f;
-    const int64_t row_slot = e4::ld(a.slots, b, t);
+
+  f32x4 st[4];
+  auto load_slot = [&](int64_t slot) {  // a stored state (zeros for the pad slot), this lane's elements
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = 4 * (lr + LPR * j);
-      f32x4 Bv, Cv;
-      if (a.in_dtype == EAGLE4_F32) {
-        Bv = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.B) + bo + n);
-        Cv = *reinterpret_cast<const f32x4*>(static_cast<const float*>(a.C) + co + n);
-      } else if (a.in_dtype == EAGLE4_BF16) {
-        Bv = load4<e4::Bf16>(static_cast<const uint16_t*>(a.B) + bo + n);
-        Cv = load4<e4::Bf16>(static_cast<const uint16_t*>(a.C) + co + n);
-      } else {
-        Bv = load4<e4::F16>(static_cast<const uint16_t*>(a.B) + bo + n);
-        Cv = load4<e4::F16>(static_cast<const uint16_t*>(a.C) + co + n);
+      st[j] = (slot != pad && mok) ? load4<S>(hstate + slot * a.stride_state_slot + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  // the prologue issues its loads before its first wait: the start state, the plan tables, the staged nodes
+  const int64_t init_row =
+      a.num_accepted.ptr != nullptr ? (e4::ld(a.num_accepted, b) - 1 > 0 ? e4::ld(a.num_accepted, b) - 1 : 0) : 0;
+  load_slot(uni64(e4::ld(a.slots, b, init_row)));
+  int par = -1;
+  int64_t my_slot = pad;
+  if (lane < T && lane < 64) {
+    par = static_cast<int>(e4::ld(a.parents, b, lane));
+    my_slot = e4::ld(a.slots, b, lane);
+  }
+  const int ts = T < TS ? T : TS;
+  for (int i = tid; i < ts * (DS / 4); i += NT) {  // B and C of the staged nodes, fp32
+    const int t = i / (DS / 4), n = 4 * (i % (DS / 4));
+    const int64_t tok = bos + t;
+    *reinterpret_cast<f32x4*>(&s_B[t][n]) = load_in4(a.B, tok * a.stride_B_tok + g * a.stride_B_group + n, a.in_dtype);
+    *reinterpret_cast<f32x4*>(&s_C[t][n]) = load_in4(a.C, tok * a.stride_C_tok + g * a.stride_C_group + n, a.in_dtype);
+  }
+  for (int i = tid; i < ts * ROWS; i += NT) {  // x of the workgroup's rows
+    const int t = i / ROWS, r = i % ROWS;
+    s_x[t][r] = row0 + r < a.head_dim
+                    ? e4::load_scalar(a.x, (bos + t) * a.stride_x_tok + h * a.stride_x_head + row0 + r, a.in_dtype)
+                    : 0.f;
+  }
+  if (tid < ts) {
+    float dt = e4::load_scalar(a.dt, (bos + tid) * a.stride_dt_tok + h * a.stride_dt_head, a.dt_dtype) + dtb;
+    if (a.dt_softplus) dt = softplus(dt);
+    s_g[tid] = make_float2(dt, exp2f(1.4426950408889634f * (A * dt)));
+  }
+
+  // the walk plan (lane i: row i): depth first when the reloads are guaranteed to return the parent's own state
+  uint64_t kids = 0;
+  int first = -1, after = -1;  // lane u: u's first child in walk order; the sibling walked after u (-1: none)
+  bool dfs = T <= 64;
+  if (dfs) {
+    bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot == pad);
+    for (int j = 0; j < T; ++j) {
+      const uint64_t sj = readlane64(static_cast<uint64_t>(my_slot), j);
+      bad = bad || (lane < T && lane != j && static_cast<uint64_t>(my_slot) == sj);
+    }
+    dfs = __ballot(bad) == 0;
+  }
+  if (dfs) {
+    for (int i = 0; i + 1 < T; ++i) {
+      const uint64_t mk = __ballot(lane > 0 && lane < T && par == i);
+      if (lane == i) kids = mk;
+    }
+    // children in increasing (need, index) with an fp32 pool, by index with a 16-bit one
+    int need = 0, m1 = 0, m2 = -1, nk = 0;  // lane u: u's need; the two largest needs among its children, their count
+    for (int i = T - 1; i >= 1; --i) {     // children before parents (rows are parent first)
+      const int nki = readlane(nk, i), m1i = readlane(m1, i), m2i = readlane(m2, i);
+      const int needi = nki == 0 ? 0 : (nki == 1 ? m1i : (m1i > m2i + 1 ? m1i : m2i + 1));
+      if (lane == i) need = needi;
+      if (lane == readlane(par, i)) {
+        ++nk;
+        if (needi > m1) {
+          m2 = m1;
+          m1 = needi;
+        } else if (needi > m2) {
+          m2 = needi;
+        }
       }
-      const f32x4 dB = Bv * dt;
-      s[j] = s[j] * dA + dB * x;
-      if (row_slot != pad && mok) store4<S>(hstate + row_slot * a.stride_state_slot + n, s[j]);
-      const f32x4 sc = s[j] * Cv;
+    }
+    const int key = (kExact ? need * 64 : 0) + lane;
+    int after_key = 1 << 30, first_key = 1 << 30;
+    for (int j = 1; j < T; ++j) {
+      const int kj = readlane(key, j), pj = readlane(par, j);
+      if (pj == par && kj > key && kj < after_key) after_key = kj;
+      if (pj == lane && kj < first_key) first_key = kj;
+    }
+    after = after_key == 1 << 30 ? -1 : (after_key & 63);
+    first = first_key == 1 << 30 ? -1 : (first_key & 63);
+  }
+  settle_loads();
+  __syncthreads();  // the staged nodes
+
+  // node t's (dt, exp(A dt)), x and B / C chunks: staged, or (past TS) from global memory, settled here
+  auto node_in = [&](int t, float2& gd, float& x, f32x4 (&Bv)[4], f32x4 (&Cv)[4]) {
+    if (t < TS) {
+      gd = s_g[t];
+      x = s_x[t][lrow];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = 4 * (lr + LPR * j);
+        Bv[j] = *reinterpret_cast<const f32x4*>(&s_B[t][n]);
+        Cv[j] = *reinterpret_cast<const f32x4*>(&s_C[t][n]);
+      }
+    } else {
+      const int64_t tok = bos + t;
+      float dt = e4::load_scalar(a.dt, tok * a.stride_dt_tok + h * a.stride_dt_head, a.dt_dtype) + dtb;
+      x = mok ? e4::load_scalar(a.x, tok * a.stride_x_tok + h * a.stride_x_head + m, a.in_dtype) : 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = 4 * (lr + LPR * j);
+        Bv[j] = load_in4(a.B, tok * a.stride_B_tok + g * a.stride_B_group + n, a.in_dtype);
+        Cv[j] = load_in4(a.C, tok * a.stride_C_tok + g * a.stride_C_group + n, a.in_dtype);
+      }
+      settle_loads();
+      if (a.dt_softplus) dt = softplus(dt);
+      gd = make_float2(dt, exp2f(1.4426950408889634f * (A * dt)));
+    }
+  };
+
+  f32x4 (*const my_stack)[4][64] = s_stack[wave];
+  int u = 0, sp = 0;
+  uint64_t unparked = 0;  // nodes with several children that found the stack full
+  for (int it = 0; it < T; ++it) {
+    // the next node
+    int next = -1;
+    bool next_first = false, next_last = false;
+    if (dfs) {
+      const int fc = readlane(first, u);
+      if (fc >= 0) {
+        next = fc;
+        next_first = true;
+      } else {
+        for (int x = u; x != 0; x = readlane(par, x)) {
+          const int sx = readlane(after, x);
+          if (sx >= 0) {
+            next = sx;
+            next_last = readlane(after, sx) < 0;
+            break;
+          }
+        }
+      }
+    } else if (u + 1 < T) {
+      next = u + 1;
+    }
+
+    // the selective state update of row u (:62-80): s = s exp(A dt) + dt B x; out = C . s + D x
+    float2 gd;
+    float x;
+    f32x4 Bv[4], Cv[4];
+    node_in(u, gd, x, Bv, Cv);
+    const int64_t tok = bos + u;
+    const int64_t row_slot = dfs ? static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), u))
+                                 : uni64(e4::ld(a.slots, b, u));
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = 4 * (lr + LPR * j);
+      st[j] = st[j] * gd.y + (Bv[j] * gd.x) * x;
+      if (row_slot != pad && mok) store4<S>(hstate + row_slot * a.stride_state_slot + n, st[j]);
+      const f32x4 sc = st[j] * Cv[j];
       part += (sc.x + sc.y) + (sc.z + sc.w);
     }
 #pragma unroll
     for (int w = LPR / 2; w > 0; w >>= 1) part += __shfl_xor(part, w);
     if (lr == 0 && mok)
       e4::store_scalar(a.out, tok * a.stride_out_tok + h * a.stride_out_head + m, a.out_dtype, part + x * Dh);
+
+    // the state the next row starts from
+    if (next >= 0) {
+      if (dfs) {
+        const uint64_t ku = readlane64(kids, u);
+        if ((ku & (ku - 1)) != 0) {  // several children: park the state, as a reload would give it, for the later ones
+          if (sp < kStack) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              f32x4 w = st[j];
+              if constexpr (!kExact)
+                w = f32x4{e4::round_through<S>(w.x), e4::round_through<S>(w.y), e4::round_through<S>(w.z),
+                          e4::round_through<S>(w.w)};
+              my_stack[sp][j][lane] = w;
+            }
+            ++sp;
+          } else {
+            unparked |= 1ull << u;
+          }
+        }
+        if (next_first) {
+          if constexpr (!kExact) {
+            if (next != u + 1) {  // not the chain child: it starts from the stored (rounded) state
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                st[j] = f32x4{e4::round_through<S>(st[j].x), e4::round_through<S>(st[j].y),
+                              e4::round_through<S>(st[j].z), e4::round_through<S>(st[j].w)};
+            }
+          }
+        } else {
+          const int p = readlane(par, next);
+          if ((unparked >> p) & 1) {
+            load_slot(static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), p)));
+            settle_loads();
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) st[j] = my_stack[sp - 1][j][lane];
+            if (next_last) --sp;
+          }
+        }
+      } else {
+        // the reference's rule (:56-61): a row whose parent is not the previous row reloads the parent's slot
+        const int64_t p = uni64(e4::ld(a.parents, b, next));
+        if (p != next - 1) {
+          load_slot(uni64(e4::ld(a.slots, b, p)));
+          settle_loads();
+        }
+      }
+    }
+    u = next;
   }
 }
 

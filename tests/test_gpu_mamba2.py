@@ -83,6 +83,20 @@ def test_other_state_sizes_and_fp16(dev, shape):
     _case(dev, shape, [_tree("tree", 12, rng), _tree("tree", 7, rng)], seed=7, in_dtype=torch.float16)
 
 
+# A complete binary tree (16 nodes): walked neediest-child-last it needs three parked states, one more than the stack
+# holds; nodes 0..5 with two children each, the lower-index one leading deeper: in index order (16-bit pools) six
+# states are parked at once. Both make the walk reload states from their slots.
+BINARY = [-1] + [(i - 1) // 2 for i in range(1, 16)]
+NESTED = [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5]
+
+
+@pytest.mark.parametrize("shape", ["tp4", "super-tp4", "d256"])
+def test_trees_beyond_the_parked_states(dev, shape):
+    announce(f"mamba2 parked-state overflow {shape}")
+    rng = random.Random(11)
+    _case(dev, shape, [BINARY, NESTED, _tree("tree", 16, rng), [-1] + [0] * 15], seed=13)
+
+
 def test_accepted_counts_pads_and_ragged_requests(dev):
     """Row 0 of each request from slots[b, accepted - 1]; pad slots neither written nor read (zeros); an empty
     request between two others."""

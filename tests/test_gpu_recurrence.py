@@ -91,10 +91,15 @@ def test_vllm_row_slots_fp32_match_oracle(dev, parent_lists, dims):
 NESTED = [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5]
 
 
+# A complete binary tree: walked neediest-child-last (fp32 snapshots) it needs three parked states, one more than the
+# stack holds, so the deepest branch points reload their snapshots.
+BINARY = [-1] + [(i - 1) // 2 for i in range(1, 16)]
+
+
 @pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
 def test_nested_branches_beyond_the_parked_states(dev, state_dtype):
     announce(f"recurrence nested branches {state_dtype}")
-    _vllm_case(dev, [NESTED, _random_tree(16, 4)], (2, 4, 128, 128), state_dtype=state_dtype)
+    _vllm_case(dev, [NESTED, BINARY, _random_tree(16, 4), [-1] + [0] * 15], (2, 4, 128, 128), state_dtype=state_dtype)
 
 
 def _pad_row(slots):
