@@ -5,7 +5,10 @@
 // (a thread per channel for the roll, an 8-channel octet per thread and node for the outputs). It stages the block's
 // node inputs (token-major, 16 bytes per 8 channels, LDS DMA when the rows are 16-byte vectors), the ancestor codes,
 // the weights and the history in LDS; every thread then computes the outputs of its octet for a strided set of
-// nodes, each window gathered from LDS through the ancestor table, and the roll follows.
+// nodes, each window gathered from LDS through the ancestor table, and the roll follows. The kernel is a chain of
+// latencies (lookups, staging, outputs, roll) per workgroup, so it is sized for residency: at most 64 VGPRs and
+// ~20 KB of LDS at 16 nodes and 19-column rows, eight workgroups per CU, so a batch-64 launch of 2048 workgroups is
+// resident at once.
 //
 // When the state rows are contiguous (token stride 1, channel stride = state length: the block's rows are one
 // 16-byte-aligned span of kChannels * L elements) the span is copied into LDS by direct loads, each thread reads its
@@ -58,10 +61,10 @@ E4_DEV uint16_t lane16(const uint4& v, int i) {
 E4_DEV void dma16(const void* src, char* dst) { __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0); }
 
 // LDS layout (byte offsets): node inputs [seqlen rounded up to kTokPerDma][kVecs] x 16, the state span [kChannels][L]
-// x 2 (row roll), history [3][kChannels] x 2, weights [4][kChannels] x 2, bias [kChannels] x 4, ancestor codes
-// [3][seqlen]. The weights are held as fp32 (exact: they are 16-bit values).
+// x 2 (row roll; the history columns are read from it) or history [3][kChannels] x 2 (element-wise state), weights
+// [4][kChannels] x 2 (the raw 16-bit taps), ancestor codes [3][seqlen].
 struct Lds {
-  int xs, rows, hist, wts, bias, anc, total;
+  int xs, rows, hist, wts, anc, total;
   int row_roll;  // the state span is staged in LDS and written back whole
 };
 
@@ -73,22 +76,23 @@ Lds lds_layout(const eagle4_conv_args& a) {
                (a.stride_cs_seq * 2) % 16 == 0;
   l.xs = 0;
   l.rows = (a.seqlen + kTokPerDma - 1) / kTokPerDma * 1024;
-  l.hist = l.rows + (l.row_roll ? (kChannels * a.state_len * 2 + 1023) / 1024 * 1024 : 0);
-  l.wts = l.hist + up16(3 * kChannels * 2);
-  l.bias = l.wts + up16(4 * kChannels * 4);
-  l.anc = l.bias + kChannels * 4;
+  l.hist = l.rows + (l.row_roll ? up16(kChannels * a.state_len * 2) : 0);
+  l.wts = l.hist + (l.row_roll ? 0 : up16(3 * kChannels * 2));
+  l.anc = l.wts + 4 * kChannels * 2;
   l.total = l.anc + up16(3 * a.seqlen * 4);
   return l;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
+// kFast: the common layout — contiguous 16-byte-aligned node inputs, outputs and state rows (row roll), no windows —
+// with the other paths compiled out, so the kernel fits in 64 VGPRs (eight workgroups per CU).
+template <typename T, bool kFast>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kFast ? 8 : 5)))
+void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
   extern __shared__ __attribute__((aligned(16))) char lds[];
   uint4* const xs = reinterpret_cast<uint4*>(lds + off.xs);        // [t * kVecs + v]
   uint16_t* const rows = reinterpret_cast<uint16_t*>(lds + off.rows);  // [c * L + col] (row roll)
-  uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c]
-  float* const wts = reinterpret_cast<float*>(lds + off.wts);          // [j * kChannels + c]
-  float* const bias_s = reinterpret_cast<float*>(lds + off.bias);
+  uint16_t* const hist = reinterpret_cast<uint16_t*>(lds + off.hist);  // [j * kChannels + c] (element-wise state)
+  uint16_t* const wts = reinterpret_cast<uint16_t*>(lds + off.wts);    // [j * kChannels + c]
   int* const anc = reinterpret_cast<int*>(lds + off.anc);             // [j * n + t]
   const int seq = blockIdx.y;
   const int cb = blockIdx.x * kChannels;
@@ -117,14 +121,14 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
 
   // ---- stage: the state span, node inputs, ancestor codes, weights, bias ------------------------------------------
   const int span = kChannels * L / 8;  // 16-byte pieces of the block's state rows (row roll)
-  if (off.row_roll) {  // instruction k fills pieces 64 k .. 64 k + 63 (past the span: its last piece again)
+  const bool row_roll = kFast || off.row_roll;
+  if (row_roll) {  // instruction k fills pieces 64 k .. 64 k + 63 (lanes past the span are off)
     for (int k = wave; 64 * k < span; k += kThreads / 64) {
-      const int i = 64 * k + lane < span ? 64 * k + lane : span - 1;
-      dma16(reinterpret_cast<const char*>(state) + 16 * i, lds + off.rows + k * 1024);
+      if (64 * k + lane < span) dma16(reinterpret_cast<const char*>(state) + 16 * (64 * k + lane), lds + off.rows + k * 1024);
     }
   }
-  const bool xvec = a.stride_x_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
-                    ((a.stride_x_token | a.stride_x_seq | cb) & 7) == 0;
+  const bool xvec = kFast || (a.stride_x_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                              ((a.stride_x_token | a.stride_x_seq | cb) & 7) == 0);
   if (xvec) {  // instruction m fills tokens kTokPerDma m .. + kTokPerDma - 1 (past the last token: the last again)
     for (int m = wave; kTokPerDma * m < n; m += kThreads / 64) {
       const int t0 = kTokPerDma * m + lane / kVecs, t = t0 < n ? t0 : n - 1;
@@ -147,67 +151,68 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
     const uint16_t* wsrc = static_cast<const uint16_t*>(a.weight) + static_cast<int64_t>(cb) * a.stride_w_dim;
     for (int i = tid; i < 4 * kChannels; i += kThreads) {
       const int c = tap_fast ? i / 4 : i % kChannels, j = tap_fast ? i % 4 : i / kChannels;
-      wts[j * kChannels + c] = c < nch ? T::to_f32(wsrc[c * a.stride_w_dim + j * a.stride_w_width]) : 0.f;
+      wts[j * kChannels + c] = c < nch ? wsrc[c * a.stride_w_dim + j * a.stride_w_width] : 0;
     }
-    for (int c = tid; c < kChannels; c += kThreads)
-      bias_s[c] = (c < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c, a.bias_dtype) : 0.f;
   }
   const bool tok_fast = a.stride_cs_tok == 1;  // lanes along the state's contiguous dimension
-  if (off.row_roll) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the span's direct loads have landed
-    __syncthreads();
-    const int c = tid;  // this thread's channel: its history columns out of the staged span
-#pragma unroll
-    for (int j = 0; j < 3; ++j) hist[j * kChannels + c] = rows[c * L + history + j];
-  } else {
+  if (!row_roll) {
     for (int i = tid; i < 3 * kChannels; i += kThreads) {
       const int c = tok_fast ? i / 3 : i % kChannels, j = tok_fast ? i % 3 : i / kChannels;
       hist[j * kChannels + c] = c < nch ? state[c * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : 0;
     }
   }
-  if (xvec) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the nodes' direct loads have landed
+  if (xvec || row_roll) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct loads have landed
   __syncthreads();
 
   // ---- outputs: thread (token lane tl, vector v) computes channels 8 v .. 8 v + 7 of nodes tl, tl + kTokLanes, ... ---
   {
     const int v = tid % kVecs, tl = tid / kVecs;
     const int c0 = 8 * v;
-    const bool ovec = a.stride_o_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-                      ((a.stride_o_token | a.stride_o_seq | cb) & 7) == 0;
+    const bool ovec = kFast || (a.stride_o_dim == 1 && nch == kChannels && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+                                ((a.stride_o_token | a.stride_o_seq | cb) & 7) == 0);
     uint16_t* window = nullptr;
-    if (a.window != nullptr)
+    if (!kFast && a.window != nullptr)
       window = static_cast<uint16_t*>(a.window) + e4::ld(a.window_indices, seq) * a.stride_win_seq +
                static_cast<int64_t>(cb + c0) * a.stride_win_dim;
+    float bias[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      bias[e] = (c0 + e < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c0 + e, a.bias_dtype) : 0.f;
     for (int t = tl; t < n; t += kTokLanes) {
-      float wv[4][8];  // the taps, read per node: fewer registers held over the loop
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 w0 = *reinterpret_cast<const float4*>(&wts[j * kChannels + c0]);
-        const float4 w1 = *reinterpret_cast<const float4*>(&wts[j * kChannels + c0 + 4]);
-        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wv[j][e] = w[e];
-      }
-      const float4 b0 = *reinterpret_cast<const float4*>(&bias_s[c0]);
-      const float4 b1 = *reinterpret_cast<const float4*>(&bias_s[c0 + 4]);
-      const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
       const uint4 xt = xs[t * kVecs + v];
       uint4 win[3];  // parent, grandparent, great-grandparent
 #pragma unroll
       for (int j = 0; j < 3; ++j) {
         const int code = anc[j * n + t];
         // _window_value (:95-98): history column 2 (code -1), 1 (-2), 0 (-3)
-        win[j] = code >= 0 ? xs[code * kVecs + v] : *reinterpret_cast<const uint4*>(&hist[(code + 3) * kChannels + c0]);
+        if (code >= 0) {
+          win[j] = xs[code * kVecs + v];
+        } else if (row_roll) {  // the octet's history column out of the staged rows
+          const uint16_t* hp = rows + c0 * L + history + (code + 3);
+          uint32_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = hp[e * L];
+          win[j] = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+        } else {
+          win[j] = *reinterpret_cast<const uint4*>(&hist[(code + 3) * kChannels + c0]);
+        }
       }
       uint32_t o[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         // channels e, e + 1 together; per channel the sum in the reference's order: bias, then self w3, parent w2,
-        // grandparent w1, great-grandparent w0
-        const f32x2 p3 = product2<T>(lane16(xt, e), lane16(xt, e + 1), wv[3][e], wv[3][e + 1]);
-        const f32x2 p2 = product2<T>(lane16(win[0], e), lane16(win[0], e + 1), wv[2][e], wv[2][e + 1]);
-        const f32x2 p1 = product2<T>(lane16(win[1], e), lane16(win[1], e + 1), wv[1][e], wv[1][e + 1]);
-        const f32x2 p0 = product2<T>(lane16(win[2], e), lane16(win[2], e + 1), wv[0][e], wv[0][e + 1]);
+        // grandparent w1, great-grandparent w0; the taps of the pair, one 32-bit read per tap
+        float wv[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t wp = *reinterpret_cast<const uint32_t*>(&wts[j * kChannels + c0 + e]);
+          wv[j][0] = T::to_f32(static_cast<uint16_t>(wp & 0xffffu));
+          wv[j][1] = T::to_f32(static_cast<uint16_t>(wp >> 16));
+        }
+        const f32x2 p3 = product2<T>(lane16(xt, e), lane16(xt, e + 1), wv[3][0], wv[3][1]);
+        const f32x2 p2 = product2<T>(lane16(win[0], e), lane16(win[0], e + 1), wv[2][0], wv[2][1]);
+        const f32x2 p1 = product2<T>(lane16(win[1], e), lane16(win[1], e + 1), wv[1][0], wv[1][1]);
+        const f32x2 p0 = product2<T>(lane16(win[2], e), lane16(win[2], e + 1), wv[0][0], wv[0][1]);
         float r[2];
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
@@ -246,13 +251,16 @@ __global__ __launch_bounds__(kThreads) void tree_conv_kernel(const eagle4_conv_a
   // the column is >= 0); every history read was staged before the barrier --------------------------------------------
   const int shift = static_cast<int>((num_tokens + 2 < L ? num_tokens + 2 : L) - num_tokens - 3);
   const int cols = 3 + n;  // source columns: history 0..2, then the nodes
-  if (off.row_roll) {
-    // this thread's channel: the destination columns in order (the same loop in every thread), into the staged span
+  if (row_roll) {
+    // this thread's channel: the destination columns in order (the same loop in every thread), into the staged span,
+    // once every output's history reads of the span are done; the channel's history columns are read first
+    __syncthreads();
     const int c = tid;
+    const uint16_t h0 = rows[c * L + history], h1 = rows[c * L + history + 1], h2 = rows[c * L + history + 2];
     const int lo = shift > 0 ? shift : 0, hi = cols + shift < L ? cols + shift : L;
     for (int col = lo; col < hi; ++col) {
       const int src = col - shift;
-      rows[c * L + col] = src < 3 ? hist[src * kChannels + c] : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
+      rows[c * L + col] = src == 0 ? h0 : src == 1 ? h1 : src == 2 ? h2 : lane16(xs[(src - 3) * kVecs + c / 8], c % 8);
     }
     __syncthreads();
     const uint4* staged = reinterpret_cast<const uint4*>(rows);
@@ -280,9 +288,22 @@ extern "C" int eagle4_gdn_tree_conv1d_update(const eagle4_conv_args* a, void* st
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const Lds off = lds_layout(*a);
   const dim3 grid(e4::ceil_div(a->dim, kChannels), a->batch);
-  if (a->dtype == EAGLE4_BF16)
-    tree_conv_kernel<e4::Bf16><<<grid, kThreads, off.total, s>>>(*a, off);
-  else
-    tree_conv_kernel<e4::F16><<<grid, kThreads, off.total, s>>>(*a, off);
+  // the kernel's vector conditions, for every block (dim a multiple of kChannels) and request
+  auto vec = [&](const void* p, int64_t s_dim, int64_t s_tok, int64_t s_seq) {
+    return s_dim == 1 && a->dim % kChannels == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0 && ((s_tok | s_seq) & 7) == 0;
+  };
+  const bool fast = off.row_roll && a->window == nullptr && vec(a->x, a->stride_x_dim, a->stride_x_token, a->stride_x_seq) &&
+                    vec(a->out, a->stride_o_dim, a->stride_o_token, a->stride_o_seq);
+  if (a->dtype == EAGLE4_BF16) {
+    if (fast)
+      tree_conv_kernel<e4::Bf16, true><<<grid, kThreads, off.total, s>>>(*a, off);
+    else
+      tree_conv_kernel<e4::Bf16, false><<<grid, kThreads, off.total, s>>>(*a, off);
+  } else {
+    if (fast)
+      tree_conv_kernel<e4::F16, true><<<grid, kThreads, off.total, s>>>(*a, off);
+    else
+      tree_conv_kernel<e4::F16, false><<<grid, kThreads, off.total, s>>>(*a, off);
+  }
   return E4_LAUNCH_STATUS();
 }

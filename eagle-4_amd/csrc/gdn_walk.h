@@ -26,15 +26,19 @@ E4_DEV void load4(const typename T::storage* p, float* out) {
   }
 }
 
+// Stores go through native vector types: HIP's float4 / uint2 structs compile the walk's snapshot stores with extra
+// register moves (453 against 448 us for the batch-64 walk).
 template <typename T>
 E4_DEV void store4(typename T::storage* p, const float* in) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
   if constexpr (sizeof(typename T::storage) == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(in[0], in[1], in[2], in[3]);
+    *reinterpret_cast<f32x4v*>(p) = f32x4v{in[0], in[1], in[2], in[3]};
   } else {
-    uint2 v;
+    u32x2v v;
     v.x = static_cast<uint32_t>(T::from_f32(in[0])) | (static_cast<uint32_t>(T::from_f32(in[1])) << 16);
     v.y = static_cast<uint32_t>(T::from_f32(in[2])) | (static_cast<uint32_t>(T::from_f32(in[3])) << 16);
-    *reinterpret_cast<uint2*>(p) = v;
+    *reinterpret_cast<u32x2v*>(p) = v;
   }
 }
 
