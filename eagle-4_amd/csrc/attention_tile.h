@@ -10,11 +10,24 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));  // a 16-byte MFMA operand as a native vector
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kTileKeys = 32;
 
 template <typename T>
 E4_DEV f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+  if constexpr (T::code == EAGLE4_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                  0, 0, 0);
+}
+
+// The same on native-vector operands (arrays of them stay in registers without the struct copies HIP's uint4 brings).
+template <typename T>
+E4_DEV f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
   if constexpr (T::code == EAGLE4_BF16)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                    c, 0, 0, 0);
@@ -189,26 +202,27 @@ E4_DEV void load_q(uint4 (&qreg)[D / 32], const uint16_t* qrow, bool ok, int g) 
   for (int c = 0; c < D / 32; ++c)
     qreg[c] = ok ? *reinterpret_cast<const uint4*>(qrow + 32 * c + 8 * g) : make_uint4(0, 0, 0, 0);
 }
+template <int D>
+E4_DEV void load_q(u32x4_t (&qreg)[D / 32], const uint16_t* qrow, bool ok, int g) {
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c)
+    qreg[c] = ok ? *reinterpret_cast<const u32x4_t*>(qrow + 32 * c + 8 * g) : u32x4_t{0u, 0u, 0u, 0u};
+}
 
 // The normalised output of a wave's rows: acc[dt][i] is d = 16 dt + 4 g + i.
 template <int D, typename T>
 E4_DEV void store_rows(uint16_t* orow, const f32x4_t (&acc)[D / 16], float inv, int g) {
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt) {
-    uint2 w;
-    w.x = pack2<T>(acc[dt][0] * inv, acc[dt][1] * inv);
-    w.y = pack2<T>(acc[dt][2] * inv, acc[dt][3] * inv);
-    *reinterpret_cast<uint2*>(orow + 16 * dt + 4 * g) = w;
-  }
+  for (int dt = 0; dt < D / 16; ++dt)
+    *reinterpret_cast<u32x2_t*>(orow + 16 * dt + 4 * g) =
+        u32x2_t{pack2<T>(acc[dt][0] * inv, acc[dt][1] * inv), pack2<T>(acc[dt][2] * inv, acc[dt][3] * inv)};
 }
 
 // An fp32 partial (normalised by its own sum) of a wave's rows, for the merge.
 template <int D>
 E4_DEV void store_partial(float* prow, const f32x4_t (&acc)[D / 16], float inv, int g) {
 #pragma unroll
-  for (int dt = 0; dt < D / 16; ++dt)
-    *reinterpret_cast<float4*>(prow + 16 * dt + 4 * g) =
-        make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+  for (int dt = 0; dt < D / 16; ++dt) *reinterpret_cast<f32x4_t*>(prow + 16 * dt + 4 * g) = acc[dt] * inv;
 }
 
 // ---- the streamed schedule (verify_attention_stream.hip) ------------------------------------------------------------

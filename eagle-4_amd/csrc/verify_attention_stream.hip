@@ -116,10 +116,8 @@ E4_DEV int page_div(int pos, int page, int shift) {
 }
 
 // 16 bytes from LDS byte address `addr`; the transposing 8-byte read (ds_read_b64_tr_b16) at `addr`.
-E4_DEV uint4 lds_load16(uint32_t addr) {
-  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-  const u32x4 v = *(const __attribute__((address_space(3))) u32x4*)static_cast<uintptr_t>(addr);
-  return make_uint4(v.x, v.y, v.z, v.w);
+E4_DEV u32x4_t lds_load16(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) u32x4_t*)static_cast<uintptr_t>(addr);
 }
 E4_DEV v4i16 lds_tr16(uint32_t addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)static_cast<uintptr_t>(addr));
@@ -204,7 +202,7 @@ E4_DEV uint2 lds_tr8(uint32_t addr) {
 // The reference's online-softmax step is kernels/online_softmax.py:11-24, over vllm/verify_attention.py:62-112's
 // masked scores; raising the reference lazily changes only fp32 rounding.
 template <int D, typename T>
-E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 (&q)[D / 32], f32x4_t (&acc)[D / 16],
+E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_t (&q)[D / 32], f32x4_t (&acc)[D / 16],
                          float& mref, float& lsum, float scale_log2, uint32_t vis, int g) {
   constexpr float kSlack = 16.0f;
   // operands are read in groups (K: KG chunks per key row, V: VG d-tiles), a compiler fence after each group: at
@@ -214,7 +212,7 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 
   f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int c0 = 0; c0 < D / 32; c0 += KG) {
-    uint4 kop[2][KG];
+    u32x4_t kop[2][KG];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -232,10 +230,9 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 
     const uint32_t o = 128 * (dt >> 2);
     const v4i16 lo4 = lds_tr16(stage + off.vb[0][dt & 3] + o);
     const v4i16 hi4 = lds_tr16(stage + off.vb[1][dt & 3] + o);
-    return make_uint4(__builtin_bit_cast(uint2, lo4).x, __builtin_bit_cast(uint2, lo4).y,
-                      __builtin_bit_cast(uint2, hi4).x, __builtin_bit_cast(uint2, hi4).y);
+    return __builtin_shufflevector(__builtin_bit_cast(u32x2_t, lo4), __builtin_bit_cast(u32x2_t, hi4), 0, 1, 2, 3);
   };
-  uint4 vop[VG];
+  u32x4_t vop[VG];
 #pragma unroll
   for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);  // the first group lands while the softmax runs
   asm volatile("" ::: "memory");
@@ -269,10 +266,10 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 
     lsum += p0 + p1;
     w[p] = pack2<T>(p0, p1);
   }
-  const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+  const u32x4_t pb = {w[0], w[1], w[2], w[3]};
 #pragma unroll
   for (int d0 = 0; d0 < D / 16; d0 += VG) {
-    uint4 nxt[VG];
+    u32x4_t nxt[VG];
     if (d0 + VG < D / 16) {
 #pragma unroll
       for (int i = 0; i < VG; ++i) nxt[i] = read_v(d0 + VG + i);
@@ -292,7 +289,7 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const uint4 
 // stays the unscaled softmax denominator) — so the products run on the exact e4m3 values. ks[kt] / vs[kt] hold the
 // scales of keys 16 kt + 4 g .. + 3.
 template <int D, typename T>
-E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& off, const uint4 (&q)[D / 32],
+E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& off, const u32x4_t (&q)[D / 32],
                              f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis, int g,
                              const float4 (&ks)[2], const float4 (&vs)[2]) {
   constexpr float kSlack = 16.0f;
@@ -312,7 +309,7 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
 #pragma unroll
     for (int c = 0; c < KG && c0 + c < D / 32; ++c)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(widen_fp8x8<T>(kraw[kt][c]), q[c0 + c], s[kt]);
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(kraw[kt][c])), q[c0 + c], s[kt]);
   }
   auto read_v = [&](int dt) { return lds_tr8(vst + off.vb[dt & 7] + 128 * (dt >> 3)); };
   uint2 vop[VG];
@@ -352,7 +349,7 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
     lsum += p0 + p1;
     w[p] = pack2<T>(p0 * vsc[kt][i0], p1 * vsc[kt][i0 + 1]);
   }
-  const uint4 pb = make_uint4(w[0], w[1], w[2], w[3]);
+  const u32x4_t pb = {w[0], w[1], w[2], w[3]};
 #pragma unroll
   for (int d0 = 0; d0 < D / 16; d0 += VG) {
     uint2 nxt[VG];
@@ -362,7 +359,7 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
     }
     asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(widen_fp8x8<T>(vop[i]), pb, acc[d0 + i]);
+    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(vop[i])), pb, acc[d0 + i]);
     if (d0 + VG < D / 16) {
 #pragma unroll
       for (int i = 0; i < VG; ++i) vop[i] = nxt[i];
@@ -718,12 +715,12 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   // ---- consumers ---------------------------------------------------------------------------------------------------
   const int G = p.G;
   const float scale_log2 = a.scale * 1.4426950408889634f;
-  uint4 q[D / 32];
+  u32x4_t q[D / 32];
   int64_t row_mask = 0;
   bool row_ok = false;
   int t = 0, head = 0;
   // the segment's row of this lane: Q, ancestor mask
-  auto enter = [&](const Cursor& c, uint4 (&qr)[D / 32], int64_t& mask_r, bool& ok_r, int& t_r, int& head_r) {
+  auto enter = [&](const Cursor& c, u32x4_t (&qr)[D / 32], int64_t& mask_r, bool& ok_r, int& t_r, int& head_r) {
     const int kvh = c.k / RG, rg = c.k - kvh * RG;
     const int rows = c.width < a.max_query_len ? c.width : a.max_query_len;
     const int rt = rg * C + wave;
@@ -779,7 +776,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       constexpr bool kAhead = !FP8 && D == 256;
       const bool more = x + 1 < g1;
       Cursor cn = cc;
-      uint4 qn[D / 32];
+      u32x4_t qn[D / 32];
       int64_t mask_n = 0;
       bool ok_n = false;
       int t_n = 0, head_n = 0;
