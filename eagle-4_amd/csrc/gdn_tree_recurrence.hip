@@ -106,6 +106,10 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   const uint32_t A_raw = load_raw(a.A_log, hv, a.A_log_dtype);
   const uint32_t dt_raw = load_raw(a.dt_bias, hv, a.dt_bias_dtype);
   const int T = static_cast<int>(eos - bos);
+  // A launch whose snapshots outgrow the last-level cache (MI355X: 256 MB) stores them nontemporally: regular stores
+  // leave a cache's worth of dirty lines that the next kernel's reads pay to write back (a 512 MB stream: 13 us
+  // faster to store, 39 us slower for the kernel after it). The launch's bytes from the grid and this request's nodes.
+  const bool snap_nt = static_cast<int64_t>(gridDim.x) * ROWS * K * static_cast<int64_t>(sizeof(SS)) * T > (256ll << 20);
   if (T <= 0) return;
 
   // The walk plan: lane i holds row i's parent, slot and children (a bit mask). Depth first needs reloads that
@@ -341,7 +345,14 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     }
     if (slot > a.pad_slot_id) {
       SS* dst = snap_at(slot, u);
-      if (full_tile) {
+      if (full_tile && snap_nt) {
+        const __amdgpu_buffer_rsrc_t r = e4walk::buffer_rsrc(dst, a.V * K * static_cast<int>(sizeof(SS)));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int s = 0; s < RPT; ++s)
+            e4walk::store4_buf<Tsnap, 2>(r, (rows[s] * K + 4 * c + 4 * C * j) * static_cast<int>(sizeof(SS)), &h[s][4 * j]);
+      } else if (full_tile) {
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
 #pragma unroll

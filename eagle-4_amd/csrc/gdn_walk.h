@@ -42,6 +42,28 @@ E4_DEV void store4(typename T::storage* p, const float* in) {
   }
 }
 
+// The same through a buffer resource, with cache policy AUX (2: nontemporal, which leaves no dirty line in the
+// last-level cache for the next kernel to write back). The policy is an immediate operand, so the compiler cannot
+// merge this store with a regular one on another path and drop the policy, as it does with nontemporal metadata.
+template <typename T, int AUX>
+E4_DEV void store4_buf(__amdgpu_buffer_rsrc_t r, int byte_off, const float* in) {
+  typedef unsigned u32x4v __attribute__((ext_vector_type(4)));
+  typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+  if constexpr (sizeof(typename T::storage) == 4) {
+    const u32x4v v = {__float_as_uint(in[0]), __float_as_uint(in[1]), __float_as_uint(in[2]), __float_as_uint(in[3])};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, byte_off, 0, AUX);
+  } else {
+    const u32x2v v = {static_cast<uint32_t>(T::from_f32(in[0])) | (static_cast<uint32_t>(T::from_f32(in[1])) << 16),
+                      static_cast<uint32_t>(T::from_f32(in[2])) | (static_cast<uint32_t>(T::from_f32(in[3])) << 16)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, byte_off, 0, AUX);
+  }
+}
+
+// A buffer resource over [base, base + bytes) (raw: byte offsets, 32-bit data format).
+E4_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+}
+
 // A chunk of four state values of a runtime dtype (the initial-state pool may differ from the snapshot buffer).
 E4_DEV void load4_code(const void* base, int64_t off, int dtype, float* out) {
   if (dtype == EAGLE4_F32)
