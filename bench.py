@@ -814,8 +814,7 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # A step is replayed as one HIP graph (the launches of a verify round, as a serving loop issues them), so the
-    # timing is the GPU's, not the host's Python. Each kernel's own duration comes from a graph of that kernel alone,
-    # replayed back to back between events on the replay stream.
+    # timing is the GPU's, not the host's Python; graphs are timed between events on the replay stream.
     def graph_of(fn, reps=1):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -832,11 +831,29 @@ def main() -> int:
         e1.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
+    # A part's time is taken inside steps: the parts are replayed in step order as one graph each, back to back on the
+    # launch stream with an event between every two, and synchronised only after all the steps. Every kernel so runs
+    # after the kernel it follows in a step, with the caches that one leaves (replayed alone, a kernel finds its own
+    # inputs in the 256 MB last-level cache: the walk, for one, runs ~50 us faster than in the step). The split adds
+    # an inter-graph dispatch gap per part, the parts' sum less the one-graph step time: each part is charged an equal
+    # share of it back, so the parts add up to the step.
+    def in_step_times(g_one, n_steps):
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(n_steps)]
+        for _ in range(2):
+            for n in names:
+                g_one[n].replay()
+        for m in marks:
+            for i, n in enumerate(names):
+                m[i].record()
+                g_one[n].replay()
+            m[-1].record()
+        torch.cuda.synchronize()
+        return {n: sum(m[i].elapsed_time(m[i + 1]) for m in marks) / n_steps for i, n in enumerate(names)}
+
     timing = "hip-graph replay"
     try:
         g_step = graph_of(step)
-        reps = 5  # calls per part graph, so a part's time carries no graph-launch gap
-        g_parts = {n: graph_of(parts[n], reps) for n in names}
+        g_one = {n: graph_of(parts[n]) for n in names}
         for _ in range(args.warmup):
             g_step.replay()
         torch.cuda.synchronize()
@@ -845,7 +862,10 @@ def main() -> int:
             g_step.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        per = {n: timed(g_parts[n].replay, args.steps) / reps for n in names}
+        raw = in_step_times(g_one, max(args.steps, 20))
+        gap = max(sum(raw.values()) - wall / args.steps * 1e3, 0.0) / len(names)
+        per = {n: max(raw[n] - gap, 0.0) for n in names}
+        split_overhead = sum(raw.values()) - sum(per.values())
     except RuntimeError as err:  # capture unavailable: eager launches (host time between launches included)
         timing = f"eager ({err.__class__.__name__}: graph capture failed)"
         torch.cuda.synchronize()
@@ -855,6 +875,7 @@ def main() -> int:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         per = {n: timed(parts[n], args.steps) for n in names}
+        split_overhead = 0.0
     ctx = att["context_lens"].cpu().tolist()
     nbytes = _algorithmic_bytes(B, W, dict(hq=ATTN_B64.hq, hkv=ATTN_B64.hkv, d=ATTN_B64.d, page=ATTN_B64.page),
                                 dict(h=H, hv=HV, k=K, v=V, dim=gdn["dim"]), ctx, path_len.tolist(), path_last)
@@ -886,7 +907,7 @@ def main() -> int:
                         "layer (tree conv1d + snapshot walk H16/HV32 K=V=128 fp32 states + accepted-path commit)",
             "batch": B, "tree_nodes": W, "attention_chunk": args.chunk,
             "step_hbm_bytes": step_bytes, "step_frac_of_hbm_roofline": step_bytes / (wall / args.steps) / HBM_PEAK,
-            "timing": timing,
+            "timing": timing, "split_gap_ms": split_overhead,
         },
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic},
