@@ -58,7 +58,7 @@ E4_DEV void item_of(int id, int HV, int tiles, int& n, int& hv, int& tile) {
 // walk itself issues no global loads for them: a vector load in the walk would wait for the snapshot stores before it
 // (loads and stores share the vmcnt counter), which serialises the walk on the store latency.
 template <int K, int C, int RPT, int WAVES, int S, typename Tin, typename Tsnap>
-__global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_gdn_args a, const int ahead) {
+__global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_gdn_args a) {
   constexpr int E = K / C;
   constexpr int NJ = E / 4;
   constexpr int ROWS_WAVE = RPT * (64 / C);
@@ -137,19 +137,6 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
         load_state_raw(a.h0_source, idx * a.stride_h0_source + head_off + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j,
                        a.h0_dtype, h0raw[s][j]);
     }
-  // The initial state of the workgroup `ahead` launches later (one round of resident workgroups) is read into the
-  // caches by this one, a word per 64 bytes, so that it is there when that workgroup's prologue reads it: read cold, it
-  // is the longest wait of a prologue, taken while the other resident workgroups' snapshot stores keep the memory
-  // busy. Its slot is looked up with this prologue's loads; the read itself is issued after the prologue's wait and
-  // waited for only after the walk (see the end of the kernel).
-  int64_t pf_idx = 0;
-  int pf_n = 0, pf_hv = 0, pf_tile = 0;
-  const bool pf_on = ahead > 0 && blockIdx.x + ahead < gridDim.x;
-  if (pf_on) {
-    item_of(blockIdx.x + ahead, a.HV, (a.V + ROWS - 1) / ROWS, pf_n, pf_hv, pf_tile);
-    const int64_t naccf = a.num_accepted.ptr != nullptr ? e4::ld(a.num_accepted, pf_n) : 1;
-    pf_idx = e4::ld(a.h0_indices, pf_n, naccf - 1);
-  }
   const int ts = T < TS ? T : TS;
   Staging<Tin, K, TS, ROWS, NT> stg;
   const NodeSrc src{a.q, a.k, a.v, a.a, a.b, a.stride_q, a.stride_k, a.stride_v, a.stride_a, a.stride_b,
@@ -223,21 +210,6 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __syncthreads();  // the raw rows' space becomes the stack
 
   settle_loads();  // the initial state and the plan tables
-  // the prefetch: one load instruction per wave (lanes past the workgroup's rows, or with nothing to prefetch, read
-  // the request table instead), from inline assembly so that the compiler neither drops the unused word nor waits for
-  // it; `pf` stays allocated until the wait at the end
-  int pf;
-  {
-    const int esize = a.h0_dtype == EAGLE4_F32 ? 4 : 2;
-    const int rowsf = a.V - pf_tile * ROWS < ROWS ? a.V - pf_tile * ROWS : ROWS;
-    const void* addr = a.cu_seqlens.ptr;
-    if (pf_on && pf_idx > a.pad_slot_id && 64 * tid < rowsf * K * esize)
-      addr = static_cast<const char*>(a.h0_source) +
-             (pf_idx * a.stride_h0_source + static_cast<int64_t>(pf_hv) * a.V * K + static_cast<int64_t>(pf_tile) * ROWS * K) * esize +
-             64 * tid;
-    asm volatile("global_load_dword %0, %1, off" : "=v"(pf) : "v"(addr) : "memory");
-  }
-  int stored = 0;  // snapshot store instructions this wave issued after the prefetch (a lower bound)
   // A node's inputs: staged nodes from LDS, later ones (T > TS) from global memory with their scalars computed here.
   auto fetch = [&](NodeIn<E, RPT, IS>& nd, int u) {
     if (u < TS) {
@@ -373,7 +345,6 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     }
     if (slot > a.pad_slot_id) {
       SS* dst = snap_at(slot, u);
-      if (full_tile) stored += NJ * RPT;
       if (full_tile && snap_nt) {
         const __amdgpu_buffer_rsrc_t r = e4walk::buffer_rsrc(dst, a.V * K * static_cast<int>(sizeof(SS)));
 #pragma unroll
@@ -460,47 +431,21 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     }
     u = next;
   }
-  // The prefetch has landed once at most `stored` younger operations are in flight (vector memory operations retire
-  // in issue order); the last nodes' stores may stay in flight. Then `pf` may be released.
-  if (stored >= 32)
-    asm volatile("s_waitcnt vmcnt(32)" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  asm volatile("" ::"v"(pf));
-}
-
-// Workgroups of `kernel` resident on the current device at once (CUs x workgroups per CU), looked up once per device;
-// 0 when the runtime cannot say.
-template <typename F>
-int resident_groups(F kernel, int threads) {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return 0;
-    cached[dev] = per_cu * cus > 0 ? per_cu * cus : -1;
-  }
-  return cached[dev] > 0 ? cached[dev] : 0;
-}
-
-template <int K, int C, int RPT, int WAVES, int S, typename Tin, typename Tsnap>
-int launch_walk(const eagle4_gdn_args& a, hipStream_t s) {
-  constexpr int ROWS = WAVES * RPT * (64 / C);
-  const dim3 grid(e4::ceil_div(a.V, ROWS) * a.HV * a.N);
-  const auto kernel = gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, Tsnap>;
-  kernel<<<grid, 64 * WAVES, 0, s>>>(a, resident_groups(kernel, 64 * WAVES));
-  return E4_LAUNCH_STATUS();
 }
 
 template <int K, int C, int RPT, int WAVES, int S, typename Tin>
 int launch_snap(const eagle4_gdn_args& a, hipStream_t s) {
-  if (a.snap_dtype == EAGLE4_F32) return launch_walk<K, C, RPT, WAVES, S, Tin, e4::F32>(a, s);
-  if (a.snap_dtype == EAGLE4_BF16) return launch_walk<K, C, RPT, WAVES, S, Tin, e4::Bf16>(a, s);
-  if (a.snap_dtype == EAGLE4_F16) return launch_walk<K, C, RPT, WAVES, S, Tin, e4::F16>(a, s);
-  return EAGLE4_NOT_COVERED;
+  constexpr int ROWS = WAVES * RPT * (64 / C);
+  const dim3 grid(e4::ceil_div(a.V, ROWS) * a.HV * a.N);
+  if (a.snap_dtype == EAGLE4_F32)
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
+  else if (a.snap_dtype == EAGLE4_BF16)
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
+  else if (a.snap_dtype == EAGLE4_F16)
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
+  else
+    return EAGLE4_NOT_COVERED;
+  return E4_LAUNCH_STATUS();
 }
 
 template <int K, int C, int RPT, int WAVES, int S>
