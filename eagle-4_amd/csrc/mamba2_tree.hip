@@ -95,6 +95,11 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   const int64_t bos = uni64(e4::ld(a.query_start_loc, b));
   const int T = static_cast<int>(uni64(e4::ld(a.query_start_loc, b + 1)) - bos);
   if (T <= 0) return;
+  // A launch whose stored states outgrow the last-level cache (MI355X: 256 MB) stores them nontemporally: regular
+  // stores leave a cache's worth of dirty lines that the next kernel's reads pay to write back. The launch's bytes from
+  // the grid and this request's nodes.
+  const bool state_nt = static_cast<int64_t>(gridDim.x) * gridDim.y * gridDim.z * T * ROWS * DS *
+                            static_cast<int64_t>(sizeof(SS)) > (256ll << 20);
   const int g = h / (a.heads / a.groups);
   const int64_t pad = a.pad_slot_id;
   SS* const hstate = static_cast<SS*>(a.state) + h * a.stride_state_head + static_cast<int64_t>(m) * a.stride_state_dim;
@@ -251,7 +256,17 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
     for (int j = 0; j < 4; ++j) {
       const int n = 4 * (lr + LPR * j);
       st[j] = st[j] * gd.y + (Bv[j] * gd.x) * x;
-      if (row_slot != pad && mok) store4<S>(hstate + row_slot * a.stride_state_slot + n, st[j]);
+      if (row_slot != pad && mok) {
+        if (state_nt) {  // buffer stores: the nt policy is an immediate the compiler cannot merge away
+          SS* const head = static_cast<SS*>(a.state) + h * a.stride_state_head + row_slot * a.stride_state_slot;
+          const int bytes = static_cast<int>(((a.head_dim - 1) * a.stride_state_dim + DS) * sizeof(SS));
+          const float w[4] = {st[j].x, st[j].y, st[j].z, st[j].w};
+          e4walk::store4_buf<S, 2>(e4walk::buffer_rsrc(head, bytes),
+                                   static_cast<int>((static_cast<int64_t>(m) * a.stride_state_dim + n) * sizeof(SS)), w);
+        } else {
+          store4<S>(hstate + row_slot * a.stride_state_slot + n, st[j]);
+        }
+      }
       const f32x4 sc = st[j] * Cv[j];
       part += (sc.x + sc.y) + (sc.z + sc.w);
     }
