@@ -831,29 +831,28 @@ def main() -> int:
         e1.synchronize()
         return e0.elapsed_time(e1) / n  # ms
 
-    # A part's time is taken inside steps: the parts are replayed in step order as one graph each, back to back on the
-    # launch stream with an event between every two, and synchronised only after all the steps. Every kernel so runs
-    # after the kernel it follows in a step, with the caches that one leaves (replayed alone, a kernel finds its own
-    # inputs in the 256 MB last-level cache: the walk, for one, runs ~50 us faster than in the step). The split adds
-    # an inter-graph dispatch gap per part, the parts' sum less the one-graph step time: each part is charged an equal
-    # share of it back, so the parts add up to the step.
-    def in_step_times(g_one, n_steps):
-        marks = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(n_steps)]
-        for _ in range(2):
+    # A part's time is what it adds to the step: T(step) - T(step without it), both one graph replayed back to back
+    # (the positions copy stays in every variant, so the stage always reads the same positions). Every kernel so runs
+    # between the kernels it has in the step, with the caches they leave: replayed alone, a kernel finds its own inputs
+    # in the 256 MB last-level cache (the walk runs ~50 us faster alone), and split into one graph per part, the
+    # dispatch gaps between the graphs let the cache write back the previous part's dirty lines (~30 us for the walk).
+    # Graph-launch overhead cancels in the difference.
+    def without(skip):
+        def run():
             for n in names:
-                g_one[n].replay()
-        for m in marks:
-            for i, n in enumerate(names):
-                m[i].record()
-                g_one[n].replay()
-            m[-1].record()
-        torch.cuda.synchronize()
-        return {n: sum(m[i].elapsed_time(m[i + 1]) for m in marks) / n_steps for i, n in enumerate(names)}
+                if n == skip:
+                    continue
+                if n == "commit":
+                    commit.commit(idx, path_d, path_len_d)  # the commit part without its positions copy
+                else:
+                    parts[n]()
+            positions.copy_(chain_pos)
+        return run
 
     timing = "hip-graph replay"
     try:
         g_step = graph_of(step)
-        g_one = {n: graph_of(parts[n]) for n in names}
+        g_less = {n: graph_of(without(n)) for n in names}
         for _ in range(args.warmup):
             g_step.replay()
         torch.cuda.synchronize()
@@ -862,10 +861,9 @@ def main() -> int:
             g_step.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        raw = in_step_times(g_one, max(args.steps, 20))
-        gap = max(sum(raw.values()) - wall / args.steps * 1e3, 0.0) / len(names)
-        per = {n: max(raw[n] - gap, 0.0) for n in names}
-        split_overhead = sum(raw.values()) - sum(per.values())
+        reps = max(args.steps, 30)
+        t_step = timed(g_step.replay, reps)
+        per = {n: t_step - timed(g_less[n].replay, reps) for n in names}
     except RuntimeError as err:  # capture unavailable: eager launches (host time between launches included)
         timing = f"eager ({err.__class__.__name__}: graph capture failed)"
         torch.cuda.synchronize()
@@ -875,7 +873,6 @@ def main() -> int:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         per = {n: timed(parts[n], args.steps) for n in names}
-        split_overhead = 0.0
     ctx = att["context_lens"].cpu().tolist()
     nbytes = _algorithmic_bytes(B, W, dict(hq=ATTN_B64.hq, hkv=ATTN_B64.hkv, d=ATTN_B64.d, page=ATTN_B64.page),
                                 dict(h=H, hv=HV, k=K, v=V, dim=gdn["dim"]), ctx, path_len.tolist(), path_last)
@@ -907,7 +904,7 @@ def main() -> int:
                         "layer (tree conv1d + snapshot walk H16/HV32 K=V=128 fp32 states + accepted-path commit)",
             "batch": B, "tree_nodes": W, "attention_chunk": args.chunk,
             "step_hbm_bytes": step_bytes, "step_frac_of_hbm_roofline": step_bytes / (wall / args.steps) / HBM_PEAK,
-            "timing": timing, "split_gap_ms": split_overhead,
+            "timing": timing, "parts_sum_ms": sum(per.values()),
         },
         "roofline": {"kernel": dominant, "bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK, "traffic": traffic},
