@@ -683,7 +683,8 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # the GPU takes ~30 step replays (~25 ms) to reach its steady step time (the first 10 run ~8 % slower)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--chunk", type=int, default=0, help="attention context keys per split (0: the library's)")
     ap.add_argument("--cpu-sample", type=int, default=64, help="requests in the CPU baseline's sample (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="the CPU baseline runs whole passes this long")
