@@ -31,6 +31,7 @@
 // node in the prologue and kept in LDS as fp32.
 
 #include "gdn_walk.h"
+#include "walk_plan.h"
 
 namespace {
 
@@ -79,6 +80,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __shared__ float4 s_sc[TS];  // decay, beta, scale / |q|, 1 / |k|
   auto& s_qr = *reinterpret_cast<IS(*)[TS][K]>(s_stack);
   auto& s_kr = *reinterpret_cast<IS(*)[TS][K]>(s_stack + TS * K * sizeof(IS));
+  // The walk plan's scratch while wave 0 builds it and hands it over: in s_q, which is first written after the
+  // staged rows are normalised, where it fits.
+  constexpr bool kPlanInQ = sizeof(float) * TS * K >= sizeof(PlanScratch);
+  __shared__ __align__(16) char s_plan_own[kPlanInQ ? 16 : sizeof(PlanScratch)];
+  PlanScratch& ps = *reinterpret_cast<PlanScratch*>(kPlanInQ ? reinterpret_cast<char*>(&s_q[0][0]) : s_plan_own);
 
   int n, hv, tile;
   item_of(blockIdx.x, a.HV, (a.V + ROWS - 1) / ROWS, n, hv, tile);
@@ -99,10 +105,12 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   }
   // The prologue issues every load before its first wait: the request's tables, the plan tables (parents, slots),
   // the initial state, the staged nodes' inputs; the plan is computed while the last of them are in flight.
-  const int64_t bos = uni64(e4::ld(a.cu_seqlens, n));
-  const int64_t eos = uni64(e4::ld(a.cu_seqlens, n + 1));
-  const int64_t cache_idx = uni64(e4::ld(a.snap_indices, n, 0));  // the request's scratch row (per-row slots: row 0's)
-  const int64_t nacc = a.num_accepted.ptr != nullptr ? uni64(e4::ld(a.num_accepted, n)) : 1;
+  const bool has_acc = a.num_accepted.ptr != nullptr;
+  const int64_t bos = uni64(e4::ld_flat(a.cu_seqlens, n));
+  const int64_t eos = uni64(e4::ld_flat(a.cu_seqlens, n + 1));
+  const int64_t cache_idx = uni64(e4::ld_flat(a.snap_indices, n, 0));  // the request's scratch row (per-row slots: row 0's)
+  const int64_t acc_raw = uni64(e4::ld_flat(has_acc ? a.num_accepted : a.cu_seqlens, n));  // loaded either way: no branch
+  const int64_t nacc = has_acc ? acc_raw : 1;
   const uint32_t A_raw = load_raw(a.A_log, hv, a.A_log_dtype);
   const uint32_t dt_raw = load_raw(a.dt_bias, hv, a.dt_bias_dtype);
   const int T = static_cast<int>(eos - bos);
@@ -112,19 +120,15 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   const bool snap_nt = static_cast<int64_t>(gridDim.x) * ROWS * K * static_cast<int64_t>(sizeof(SS)) * T > (256ll << 20);
   if (T <= 0) return;
 
-  // The walk plan: lane i holds row i's parent, slot and children (a bit mask). Depth first needs reloads that
-  // return the parent's own snapshot.
+  // Lane i holds row i's parent and slot (rows of at most 64-row requests).
   int par = 0;
   int64_t my_slot = cache_idx;
-  uint64_t kids = 0;
-  int first = -1, after = -1;  // lane u: u's first child in walk order; the sibling walked after u (-1: none)
-  bool dfs = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
-  if (dfs && lane < T) {
-    par = static_cast<int>(e4::ld(a.parents, n, lane));
-    if (a.row_slots) my_slot = e4::ld(a.snap_indices, n, lane);
+  if (T <= 64 && lane < T) {
+    par = static_cast<int>(e4::ld_flat(a.parents, n, lane));
+    if (a.row_slots) my_slot = e4::ld_flat(a.snap_indices, n, lane);
   }
   // the initial state (:284-296); with num_accepted its slot is in column num_accepted - 1
-  const int64_t idx = uni64(e4::ld(a.h0_indices, n, nacc - 1));
+  const int64_t idx = uni64(e4::ld_flat(a.h0_indices, n, nacc - 1));
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
   float h[RPT][E];
   u32x4 h0raw[RPT][NJ];
@@ -143,51 +147,19 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
                     a.gate_dtype, ih, hv, a.V};
   stg.issue(src, bos, ts, row0, tid);
 
-  if (dfs) {
-    bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot <= a.pad_slot_id);
-    if (a.row_slots) {
-      for (int j = 0; j < T; ++j) {
-        const uint64_t sj = readlane64(static_cast<uint64_t>(my_slot), j);
-        bad = bad || (lane < T && lane != j && static_cast<uint64_t>(my_slot) == sj);
-      }
+  // The walk plan (walk_plan.h), built by wave 0 and read by every wave after the staging barrier. Depth first needs
+  // reloads that return the parent's own snapshot: parents before children, every row a real slot, no two rows one.
+  // Children go in increasing (need, index), except with 16-bit snapshots and the chain-child rule, where a chain
+  // child must be the first child (it continues unrounded from the registers), so that case keeps the index order.
+  if (wave == 0) {
+    bool ok = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
+    if (ok) {
+      bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot <= a.pad_slot_id);
+      if (a.row_slots) bad = bad || slot_repeats(static_cast<uint64_t>(my_slot), lane, T);
+      ok = __ballot(bad) == 0;
     }
-    dfs = __ballot(bad) == 0;
-    if (dfs) {
-      for (int i = 0; i + 1 < T; ++i) {
-        const uint64_t m = __ballot(lane > 0 && lane < T && par == i);
-        if (lane == i) kids = m;
-      }
-      // The order of the children. A node with several children holds a stack entry while its earlier children's
-      // subtrees are walked, so walking the child whose subtree needs the most entries last keeps the stack shallow:
-      // need(u) = 0 for a leaf, need(child) for one child, else max(largest, second largest + 1) over the children
-      // (Sethi-Ullman numbering). Children go in increasing (need, index); the values do not depend on the order. With
-      // 16-bit snapshots and the chain-child rule a chain child must be the first child (it continues unrounded from
-      // the registers), so that case keeps the index order.
-      int need = 0, m1 = 0, m2 = -1, nk = 0;  // lane u: u's need; the two largest needs among its children, their count
-      for (int i = T - 1; i >= 1; --i) {  // children before parents (rows are parent first)
-        const int nki = readlane(nk, i), m1i = readlane(m1, i), m2i = readlane(m2, i);
-        const int needi = nki == 0 ? 0 : (nki == 1 ? m1i : (m1i > m2i + 1 ? m1i : m2i + 1));
-        if (lane == i) need = needi;
-        if (lane == readlane(par, i)) {
-          ++nk;
-          if (needi > m1) {
-            m2 = m1;
-            m1 = needi;
-          } else if (needi > m2) {
-            m2 = needi;
-          }
-        }
-      }
-      const int key = (kExact || !a.skip_chain_reload ? need * 64 : 0) + lane;
-      int after_key = 1 << 30, first_key = 1 << 30;
-      for (int j = 1; j < T; ++j) {
-        const int kj = readlane(key, j), pj = readlane(par, j);
-        if (pj == par && kj > key && kj < after_key) after_key = kj;
-        if (pj == lane && kj < first_key) first_key = kj;
-      }
-      after = after_key == 1 << 30 ? -1 : (after_key & 63);
-      first = first_key == 1 << 30 ? -1 : (first_key & 63);
-    }
+    ps.plan[lane] = ok ? build_plan(ps, lane, T, par, kExact || !a.skip_chain_reload) : kNoNext;
+    if (lane == 0) ps.dfs = ok ? 1 : 0;
   }
 
   // ---- staging: q, k, v and the node scalars of nodes [0, ts) into LDS --------------------------------------------
@@ -199,6 +171,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
 #pragma unroll
     for (int j = 0; j < NJ; ++j) widen_state_raw(h0raw[s][j], a.h0_dtype, &h[s][4 * j]);
   __syncthreads();
+  const int plan = ps.plan[lane];  // read before s_q is written, after the next barrier
+  const bool dfs = ps.dfs != 0;
   stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
   __syncthreads();
   for (int i = tid; i < ts * K; i += NT) {  // q^ and k^, read by every node of the walk
@@ -288,26 +262,15 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   uint64_t unparked = 0;  // nodes with several children that found the stack full
   for (int it = 0; it < T; ++it) {
     // the next node and where its state comes from
-    int next = -1;
-    bool next_first = false, next_last = false;
+    int next = -1, pl = 0;
     if (dfs) {
-      const int fc = readlane(first, u);
-      if (fc >= 0) {
-        next = fc;
-        next_first = true;
-      } else {
-        for (int x = u; x != 0; x = readlane(par, x)) {
-          const int sx = readlane(after, x);
-          if (sx >= 0) {
-            next = sx;
-            next_last = readlane(after, sx) < 0;
-            break;
-          }
-        }
-      }
+      pl = readlane(plan, u);
+      next = plan_next(pl);
+      if (next >= T) next = -1;  // (never: plan rows are the request's)
     } else if (u + 1 < T) {
       next = u + 1;
     }
+    const bool next_first = (pl & kPlanFirst) != 0, next_last = (pl & kPlanLast) != 0;
     if (next >= 0 && next < TS) fetch(nxt, next);  // staged: LDS reads only, ahead of their use
 
     // the delta rule step (:167-185): h *= decay; v' = (v - h k^) beta; h += k^ v'; o = h q^
@@ -370,8 +333,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
     // the state the next node starts from
     if (next >= 0) {
       if (dfs) {
-        const uint64_t ku = readlane64(kids, u);
-        if ((ku & (ku - 1)) != 0) {  // several children: park the state (as a reload would give it) for the later ones
+        if ((pl & kPlanMulti) != 0) {  // several children: park the state (as a reload would give it) for the later ones
           if (sp < S) {
 #pragma unroll
             for (int s = 0; s < RPT; ++s)

@@ -102,6 +102,18 @@ def test_nested_branches_beyond_the_parked_states(dev, state_dtype):
     _vllm_case(dev, [NESTED, BINARY, _random_tree(16, 4), [-1] + [0] * 15], (2, 4, 128, 128), state_dtype=state_dtype)
 
 
+COMB = [-1] + [2 * ((i - 1) // 2) for i in range(1, 64)]  # even rows a 32-row spine, every spine row with a leaf too
+
+
+@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
+def test_depth_first_plans_up_to_64_rows(dev, state_dtype):
+    """The widest depth-first requests: 64 rows (random, a 64-row chain, a deep comb) and 33 rows, whose plans need
+    every round of the plan's pointer jumping (the chain: 63 levels) and nested parked states (the comb)."""
+    announce(f"recurrence 64-row plans {state_dtype}")
+    _vllm_case(dev, [_random_tree(64, 9), list(range(-1, 63)), COMB, _random_tree(33, 10)], (1, 2, 64, 32),
+               state_dtype=state_dtype)
+
+
 def _pad_row(slots):
     slots[0, 3] = 0  # row 3's snapshot is not written; its children continue from the previous row's state
 
