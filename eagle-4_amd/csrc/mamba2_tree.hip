@@ -26,6 +26,7 @@
 // in LDS before the walk; later nodes and the rare reloads settle their own loads.
 
 #include "gdn_walk.h"
+#include "walk_plan.h"
 
 namespace {
 
@@ -34,6 +35,14 @@ using e4walk::readlane64;
 using e4walk::settle_loads;
 using e4walk::uni;
 using e4walk::uni64;
+using e4walk::PlanScratch;
+using e4walk::build_plan;
+using e4walk::kNoNext;
+using e4walk::kPlanFirst;
+using e4walk::kPlanLast;
+using e4walk::kPlanMulti;
+using e4walk::plan_next;
+using e4walk::slot_repeats;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -85,6 +94,7 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   __shared__ __align__(16) float s_C[TS][DS];
   __shared__ float s_x[TS][ROWS];
   __shared__ float2 s_g[TS];  // a staged node's (dt, exp(A dt))
+  __shared__ PlanScratch s_plan;  // the walk plan, built by wave 0
 
   const int b = blockIdx.y, h = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane % LPR;
@@ -92,8 +102,11 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   const int lrow = wave * (64 / LPR) + lane / LPR;  // the lane's row within the workgroup
   const int m = row0 + lrow;
   const bool mok = m < a.head_dim;
-  const int64_t bos = uni64(e4::ld(a.query_start_loc, b));
-  const int T = static_cast<int>(uni64(e4::ld(a.query_start_loc, b + 1)) - bos);
+  // the request's table entries, loaded together (no branch on a table's dtype)
+  const bool has_acc = a.num_accepted.ptr != nullptr;
+  const int64_t bos = uni64(e4::ld_flat(a.query_start_loc, b));
+  const int T = static_cast<int>(uni64(e4::ld_flat(a.query_start_loc, b + 1)) - bos);
+  const int64_t acc = uni64(e4::ld_flat(has_acc ? a.num_accepted : a.query_start_loc, b));  // loaded either way
   if (T <= 0) return;
   // A launch whose stored states outgrow the last-level cache (MI355X: 256 MB) stores them nontemporally: regular
   // stores leave a cache's worth of dirty lines that the next kernel's reads pay to write back. The launch's bytes from
@@ -116,15 +129,14 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
     }
   };
   // the prologue issues its loads before its first wait: the start state, the plan tables, the staged nodes
-  const int64_t init_row =
-      a.num_accepted.ptr != nullptr ? (e4::ld(a.num_accepted, b) - 1 > 0 ? e4::ld(a.num_accepted, b) - 1 : 0) : 0;
-  load_slot(uni64(e4::ld(a.slots, b, init_row)));
+  const int64_t init_row = has_acc ? (acc - 1 > 0 ? acc - 1 : 0) : 0;
   int par = -1;
   int64_t my_slot = pad;
   if (lane < T && lane < 64) {
-    par = static_cast<int>(e4::ld(a.parents, b, lane));
-    my_slot = e4::ld(a.slots, b, lane);
+    par = static_cast<int>(e4::ld_flat(a.parents, b, lane));
+    my_slot = e4::ld_flat(a.slots, b, lane);
   }
+  load_slot(uni64(e4::ld_flat(a.slots, b, init_row)));
   const int ts = T < TS ? T : TS;
   for (int i = tid; i < ts * (DS / 4); i += NT) {  // B and C of the staged nodes, fp32
     const int t = i / (DS / 4), n = 4 * (i % (DS / 4));
@@ -144,51 +156,23 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
     s_g[tid] = make_float2(dt, exp2f(1.4426950408889634f * (A * dt)));
   }
 
-  // the walk plan (lane i: row i): depth first when the reloads are guaranteed to return the parent's own state
-  uint64_t kids = 0;
-  int first = -1, after = -1;  // lane u: u's first child in walk order; the sibling walked after u (-1: none)
-  bool dfs = T <= 64;
-  if (dfs) {
-    bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot == pad);
-    for (int j = 0; j < T; ++j) {
-      const uint64_t sj = readlane64(static_cast<uint64_t>(my_slot), j);
-      bad = bad || (lane < T && lane != j && static_cast<uint64_t>(my_slot) == sj);
+  // The walk plan (walk_plan.h), built by wave 0 and read by every wave after the staging barrier: depth first when
+  // the reloads are guaranteed to return the parent's own state; children in increasing (need, index) with an fp32
+  // pool, by index with a 16-bit one.
+  if (wave == 0) {
+    bool ok = T <= 64;
+    if (ok) {
+      bool bad = lane < T && ((lane > 0 && (par < 0 || par >= lane)) || my_slot == pad);
+      bad = bad || slot_repeats(static_cast<uint64_t>(my_slot), lane, T);
+      ok = __ballot(bad) == 0;
     }
-    dfs = __ballot(bad) == 0;
-  }
-  if (dfs) {
-    for (int i = 0; i + 1 < T; ++i) {
-      const uint64_t mk = __ballot(lane > 0 && lane < T && par == i);
-      if (lane == i) kids = mk;
-    }
-    // children in increasing (need, index) with an fp32 pool, by index with a 16-bit one
-    int need = 0, m1 = 0, m2 = -1, nk = 0;  // lane u: u's need; the two largest needs among its children, their count
-    for (int i = T - 1; i >= 1; --i) {     // children before parents (rows are parent first)
-      const int nki = readlane(nk, i), m1i = readlane(m1, i), m2i = readlane(m2, i);
-      const int needi = nki == 0 ? 0 : (nki == 1 ? m1i : (m1i > m2i + 1 ? m1i : m2i + 1));
-      if (lane == i) need = needi;
-      if (lane == readlane(par, i)) {
-        ++nk;
-        if (needi > m1) {
-          m2 = m1;
-          m1 = needi;
-        } else if (needi > m2) {
-          m2 = needi;
-        }
-      }
-    }
-    const int key = (kExact ? need * 64 : 0) + lane;
-    int after_key = 1 << 30, first_key = 1 << 30;
-    for (int j = 1; j < T; ++j) {
-      const int kj = readlane(key, j), pj = readlane(par, j);
-      if (pj == par && kj > key && kj < after_key) after_key = kj;
-      if (pj == lane && kj < first_key) first_key = kj;
-    }
-    after = after_key == 1 << 30 ? -1 : (after_key & 63);
-    first = first_key == 1 << 30 ? -1 : (first_key & 63);
+    s_plan.plan[lane] = ok ? build_plan(s_plan, lane, T, par, kExact) : kNoNext;
+    if (lane == 0) s_plan.dfs = ok ? 1 : 0;
   }
   settle_loads();
-  __syncthreads();  // the staged nodes
+  __syncthreads();  // the staged nodes and the plan
+  const int plan = s_plan.plan[lane];
+  const bool dfs = s_plan.dfs != 0;
 
   // node t's (dt, exp(A dt)), x and B / C chunks: staged, or (past TS) from global memory, settled here
   auto node_in = [&](int t, float2& gd, float& x, f32x4 (&Bv)[4], f32x4 (&Cv)[4]) {
@@ -222,26 +206,15 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   uint64_t unparked = 0;  // nodes with several children that found the stack full
   for (int it = 0; it < T; ++it) {
     // the next node
-    int next = -1;
-    bool next_first = false, next_last = false;
+    int next = -1, pl = 0;
     if (dfs) {
-      const int fc = readlane(first, u);
-      if (fc >= 0) {
-        next = fc;
-        next_first = true;
-      } else {
-        for (int x = u; x != 0; x = readlane(par, x)) {
-          const int sx = readlane(after, x);
-          if (sx >= 0) {
-            next = sx;
-            next_last = readlane(after, sx) < 0;
-            break;
-          }
-        }
-      }
+      pl = readlane(plan, u);
+      next = plan_next(pl);
+      if (next >= T) next = -1;  // (never: plan rows are the request's)
     } else if (u + 1 < T) {
       next = u + 1;
     }
+    const bool next_first = (pl & kPlanFirst) != 0, next_last = (pl & kPlanLast) != 0;
 
     // the selective state update of row u (:62-80): s = s exp(A dt) + dt B x; out = C . s + D x
     float2 gd;
@@ -278,8 +251,7 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
     // the state the next row starts from
     if (next >= 0) {
       if (dfs) {
-        const uint64_t ku = readlane64(kids, u);
-        if ((ku & (ku - 1)) != 0) {  // several children: park the state, as a reload would give it, for the later ones
+        if ((pl & kPlanMulti) != 0) {  // several children: park the state, as a reload would give it, for the later ones
           if (sp < kStack) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
