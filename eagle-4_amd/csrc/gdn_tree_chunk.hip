@@ -408,10 +408,6 @@ int launch_k(const eagle4_records_args& a, hipStream_t s) {
   // K = V = 128: 1 tile per wave at 1 request, 2 at 4, 4 at 16 and 32)
   const int64_t pairs = static_cast<int64_t>(a.N) * a.HV;
   const bool fp32_pool = a.state_dtype == EAGLE4_F32;
-#ifdef E4_CHUNK_NTL
-  constexpr int forced = E4_CHUNK_NTL;
-  if (a.V % (16 * forced) == 0) return launch_pool<K, forced>(a, s);
-#endif
   if constexpr (K <= 128)
     if (!fp32_pool && a.V % 64 == 0 && pairs * (a.V / 64) >= 1024) return launch_pool<K, 4>(a, s);
   if (a.V % 32 == 0 && pairs * (a.V / 32) >= 512) return launch_pool<K, 2>(a, s);
