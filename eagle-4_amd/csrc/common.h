@@ -84,17 +84,12 @@ E4_DEV float round_code(float f, int dtype) {
 }
 
 // ---- integer tables -----------------------------------------------------------------------------------------------
+// Entry (i, j) of an integer table of either dtype, with no branch on the dtype: two dword loads (an int64 entry's
+// low and high words, or an int32 entry twice) joined by shifts; for int32, (lo:lo << 32) >> 32 is lo sign-extended.
+// Loads of several tables then sit in one basic block and are all in flight before the first wait; behind a branch
+// the compiler waits for each table before it issues the next (and a select between the two results is turned back
+// into that branch).
 E4_DEV int64_t ld(const eagle4_itab& t, int64_t i, int64_t j = 0) {
-  const int64_t off = i * t.s0 + j * t.s1;
-  if (t.dtype == EAGLE4_I64) return static_cast<const int64_t*>(t.ptr)[off];
-  return static_cast<const int32_t*>(t.ptr)[off];
-}
-
-// The same entry without a branch on the table's dtype: two dword loads (an int64 entry's low and high words, or an
-// int32 entry twice) joined by shifts. Loads of several tables then sit in one basic block and can all be in flight
-// before the first wait; behind ld()'s branch the compiler waits for each table before it issues the next. (A select
-// between the two results would be turned back into that branch.) For int32, (lo:lo << 32) >> 32 is lo sign-extended.
-E4_DEV int64_t ld_flat(const eagle4_itab& t, int64_t i, int64_t j = 0) {
   const int64_t off = i * t.s0 + j * t.s1;
   const bool wide = t.dtype == EAGLE4_I64;
   const uint32_t* p = static_cast<const uint32_t*>(t.ptr) + (wide ? 2 * off : off);

@@ -106,10 +106,10 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   // The prologue issues every load before its first wait: the request's tables, the plan tables (parents, slots),
   // the initial state, the staged nodes' inputs; the plan is computed while the last of them are in flight.
   const bool has_acc = a.num_accepted.ptr != nullptr;
-  const int64_t bos = uni64(e4::ld_flat(a.cu_seqlens, n));
-  const int64_t eos = uni64(e4::ld_flat(a.cu_seqlens, n + 1));
-  const int64_t cache_idx = uni64(e4::ld_flat(a.snap_indices, n, 0));  // the request's scratch row (per-row slots: row 0's)
-  const int64_t acc_raw = uni64(e4::ld_flat(has_acc ? a.num_accepted : a.cu_seqlens, n));  // loaded either way: no branch
+  const int64_t bos = uni64(e4::ld(a.cu_seqlens, n));
+  const int64_t eos = uni64(e4::ld(a.cu_seqlens, n + 1));
+  const int64_t cache_idx = uni64(e4::ld(a.snap_indices, n, 0));  // the request's scratch row (per-row slots: row 0's)
+  const int64_t acc_raw = uni64(e4::ld(has_acc ? a.num_accepted : a.cu_seqlens, n));  // loaded either way: no branch
   const int64_t nacc = has_acc ? acc_raw : 1;
   const uint32_t A_raw = load_raw(a.A_log, hv, a.A_log_dtype);
   const uint32_t dt_raw = load_raw(a.dt_bias, hv, a.dt_bias_dtype);
@@ -124,11 +124,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   int par = 0;
   int64_t my_slot = cache_idx;
   if (T <= 64 && lane < T) {
-    par = static_cast<int>(e4::ld_flat(a.parents, n, lane));
-    if (a.row_slots) my_slot = e4::ld_flat(a.snap_indices, n, lane);
+    par = static_cast<int>(e4::ld(a.parents, n, lane));
+    if (a.row_slots) my_slot = e4::ld(a.snap_indices, n, lane);
   }
   // the initial state (:284-296); with num_accepted its slot is in column num_accepted - 1
-  const int64_t idx = uni64(e4::ld_flat(a.h0_indices, n, nacc - 1));
+  const int64_t idx = uni64(e4::ld(a.h0_indices, n, nacc - 1));
   const int64_t head_off = static_cast<int64_t>(hv) * a.V * K;
   float h[RPT][E];
   u32x4 h0raw[RPT][NJ];

@@ -104,9 +104,9 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   const bool mok = m < a.head_dim;
   // the request's table entries, loaded together (no branch on a table's dtype)
   const bool has_acc = a.num_accepted.ptr != nullptr;
-  const int64_t bos = uni64(e4::ld_flat(a.query_start_loc, b));
-  const int T = static_cast<int>(uni64(e4::ld_flat(a.query_start_loc, b + 1)) - bos);
-  const int64_t acc = uni64(e4::ld_flat(has_acc ? a.num_accepted : a.query_start_loc, b));  // loaded either way
+  const int64_t bos = uni64(e4::ld(a.query_start_loc, b));
+  const int T = static_cast<int>(uni64(e4::ld(a.query_start_loc, b + 1)) - bos);
+  const int64_t acc = uni64(e4::ld(has_acc ? a.num_accepted : a.query_start_loc, b));  // loaded either way
   if (T <= 0) return;
   // A launch whose stored states outgrow the last-level cache (MI355X: 256 MB) stores them nontemporally: regular
   // stores leave a cache's worth of dirty lines that the next kernel's reads pay to write back. The launch's bytes from
@@ -133,10 +133,10 @@ __global__ __launch_bounds__(NT) void mamba2_tree_kernel(const eagle4_mamba2_arg
   int par = -1;
   int64_t my_slot = pad;
   if (lane < T && lane < 64) {
-    par = static_cast<int>(e4::ld_flat(a.parents, b, lane));
-    my_slot = e4::ld_flat(a.slots, b, lane);
+    par = static_cast<int>(e4::ld(a.parents, b, lane));
+    my_slot = e4::ld(a.slots, b, lane);
   }
-  load_slot(uni64(e4::ld_flat(a.slots, b, init_row)));
+  load_slot(uni64(e4::ld(a.slots, b, init_row)));
   const int ts = T < TS ? T : TS;
   for (int i = tid; i < ts * (DS / 4); i += NT) {  // B and C of the staged nodes, fp32
     const int t = i / (DS / 4), n = 4 * (i % (DS / 4));
