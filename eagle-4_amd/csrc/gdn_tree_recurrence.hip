@@ -438,7 +438,15 @@ extern "C" int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* a, void* 
     case 16: return launch_in<16, 4, 1, 4, 4>(*a, s);
     case 32: return launch_in<32, 8, 1, 4, 4>(*a, s);
     case 64: return launch_in<64, 8, 1, 4, 4>(*a, s);
-    case 128: return launch_in<128, 8, 1, 4, 2>(*a, s);
+    case 128: {
+      // 8 lanes per row, 32 rows per workgroup; a grid that leaves CUs idle that way (gfx950 parts have 256; batch 1-2
+      // at 32 value heads) takes 16 lanes per row instead: each node's dependent chains (the h k and h q sums over a
+      // lane's K values) halve and the grid doubles. Batch 1 24.3 -> 21.7 us, batch 2 25.2 -> 24.3 us; from batch 4
+      // up (4 x 32 x 4 workgroups) the 8-lane form is faster (batch 64: 375 against 396 us).
+      const int64_t groups8 = e4::ceil_div(a->V, 32) * static_cast<int64_t>(a->HV) * a->N;
+      if (groups8 <= 256) return launch_in<128, 16, 1, 4, 2>(*a, s);
+      return launch_in<128, 8, 1, 4, 2>(*a, s);
+    }
     case 256: return launch_in<256, 16, 1, 4, 2>(*a, s);
     default: return EAGLE4_NOT_COVERED;
   }
