@@ -17,7 +17,8 @@
 // written element-wise.
 //
 // State move (_move_state_kernel, :218-245): a pure HBM copy of 2 x HV V K elements per moved request and layer,
-// 16-byte loads and stores. A workgroup looks its request's slots up once and copies its split in 32 KB steps, two
+// 16-byte loads and stores; the loads with the nontemporal policy (the source, the walk's snapshot of the accepted
+// node, is read once: batch-64 step 0.775 -> 0.771 ms). A workgroup looks its request's slots up once and copies its split in 32 KB steps, two
 // steps in flight, so the lookups' latency is paid once per split rather than once per step.
 
 #include "common.h"
@@ -152,7 +153,7 @@ __device__ void move_state(const eagle4_state_commit_args& a, int64_t id, int sp
 #pragma unroll
       for (int c = 0; c < kCopies; ++c) {
         const int64_t i = i0 + (static_cast<int64_t>(c) * kThreads + tid) * 16;
-        if (i < hi) v[c] = *reinterpret_cast<gsrc*>(reinterpret_cast<uintptr_t>(src + i));
+        if (i < hi) v[c] = __builtin_nontemporal_load(reinterpret_cast<gsrc*>(reinterpret_cast<uintptr_t>(src + i)));
       }
     };
     auto store = [&](const u32x4 (&v)[kCopies], int64_t i0) {
