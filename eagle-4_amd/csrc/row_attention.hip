@@ -129,8 +129,8 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
       // the builtin takes its source as a plain pointer variable
       const char* ksrc = kc + koff + 16 * (pc ^ TL::kswz(row));
       const char* vsrc = vc + voff + 16 * (pc ^ TL::vswz(row));
-      __builtin_amdgcn_global_load_lds(ksrc, kb + n * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vsrc, vb + n * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ksrc, kb + n * 1024, 16, 0, 2);
+      __builtin_amdgcn_global_load_lds(vsrc, vb + n * 1024, 16, 0, 2);
     }
   };
 

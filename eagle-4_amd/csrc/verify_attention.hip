@@ -103,8 +103,8 @@ E4_DEV void issue_direct_ctx(char* sKb, char* sVb, const DirectPages<D, NW>& p, 
       // the builtin takes its source as a plain pointer variable (a compound expression fails its overload check)
       const char* ksrc = kv.kbase + off + 16 * (pc ^ TL::kswz(row));
       const char* vsrc = kv.vbase + offv + 16 * (pc ^ TL::vswz(row));
-      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 2);
+      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 2);
     }
   }
 }
@@ -122,8 +122,8 @@ E4_DEV void issue_direct_new(char* sKb, char* sVb, const char* knew, const char*
       const int key = first + row < width ? first + row : width - 1;
       const char* ksrc = knew + static_cast<int64_t>(key) * kstride + 16 * (pc ^ TL::kswz(row));
       const char* vsrc = vnew + static_cast<int64_t>(key) * vstride + 16 * (pc ^ TL::vswz(row));
-      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ksrc, sKb + n * 1024, 16, 0, 2);
+      __builtin_amdgcn_global_load_lds(vsrc, sVb + n * 1024, 16, 0, 2);
     }
   }
 }
