@@ -34,7 +34,12 @@ __global__ __launch_bounds__(256) void argmax_kernel(const eagle4_argmax_args a)
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       const int v = v0 + u * static_cast<int>(blockDim.x);
-      raw[u] = *reinterpret_cast<const uint4*>(p + static_cast<int64_t>(v < nvec ? v : 0) * VEC);
+      {  // read once, nontemporally: the 2.5 GB of logits do not churn the last-level cache (449 -> 397 us at 8192 rows)
+        typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));
+        const u32x4n t =
+            __builtin_nontemporal_load(reinterpret_cast<const u32x4n*>(p + static_cast<int64_t>(v < nvec ? v : 0) * VEC));
+        raw[u] = make_uint4(t.x, t.y, t.z, t.w);
+      }
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
