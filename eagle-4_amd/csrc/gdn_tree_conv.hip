@@ -266,7 +266,12 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
     __syncthreads();
     const uint4* staged = reinterpret_cast<const uint4*>(rows);
     uint4* dst = reinterpret_cast<uint4*>(state);
-    for (int i = tid; i < span; i += kThreads) dst[i] = staged[i];
+    // nontemporal: the rolled rows are read again only by the next round's conv (batch-64 step 0.740 -> 0.736 ms)
+    typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));
+    for (int i = tid; i < span; i += kThreads) {
+      const uint4 w = staged[i];
+      __builtin_nontemporal_store(u32x4n{w.x, w.y, w.z, w.w}, reinterpret_cast<u32x4n*>(dst + i));
+    }
   } else {
     for (int i = tid; i < cols * kChannels; i += kThreads) {
       const int c = tok_fast ? i / cols : i % kChannels, src = tok_fast ? i % cols : i / kChannels;
