@@ -357,7 +357,7 @@ struct Plan {
 // 16-row tiles; a workgroup takes up to 8 of them (more rows: more row groups, each reading the KV once).
 Plan plan(const eagle4_attn_args& a) {
   Plan p;
-  p.chunk = a.chunk > 0 ? a.chunk : 1024;
+  p.chunk = a.chunk > 0 ? a.chunk : (small_attention_job(a) ? kSmallJobChunk : 1024);
   const int G = a.Hq / a.Hkv;
   p.row_tiles = e4::ceil_div(static_cast<int64_t>(G) * a.max_query_len, 16);
   const int need = p.row_tiles < 8 ? p.row_tiles : 8;
@@ -381,7 +381,7 @@ bool covered(const eagle4_attn_args& a) {
   if (a.dtype != EAGLE4_BF16 && a.dtype != EAGLE4_F16) return false;
   if (a.cache_dtype != a.dtype && a.cache_dtype != EAGLE4_FP8_E4M3) return false;
   if (a.cache_dtype == EAGLE4_FP8_E4M3 && (a.k_scale == nullptr || a.v_scale == nullptr)) return false;
-  const int chunk = a.chunk > 0 ? a.chunk : 1024;
+  const int chunk = a.chunk > 0 ? a.chunk : (small_attention_job(a) ? kSmallJobChunk : 1024);
   if (chunk % kTileKeys != 0) return false;
   if (static_cast<int64_t>(a.max_blocks) * a.page >= (int64_t(1) << 31)) return false;  // 32-bit positions
   // 16-byte vector accesses along D

@@ -968,7 +968,7 @@ int with_config(const eagle4_attn_args& a, int c, F&& go) {
 // by the caller.
 bool stream_covered(const eagle4_attn_args& a) {
   const bool fp8 = a.cache_dtype == EAGLE4_FP8_E4M3 && a.k_scale != nullptr && a.v_scale != nullptr;
-  return (a.cache_dtype == a.dtype || fp8) && a.num_reqs <= kStreamMaxReqs && a.chunk <= 0;
+  return (a.cache_dtype == a.dtype || fp8) && a.num_reqs <= kStreamMaxReqs && a.chunk <= 0 && !small_attention_job(a);
 }
 
 bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
