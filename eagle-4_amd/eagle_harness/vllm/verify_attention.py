@@ -9,8 +9,8 @@ Three schedules (``csrc/``):
   workgroup per resident slot takes equal contiguous shares of all (request, KV head, row group) tiles of 32 keys
   (64 fp8 keys), streamed into LDS by producer waves; segments cut by a share boundary leave fp32 partials that a
   second kernel merges by their log-sum-exp.
-- ``verify_attention.hip`` (more requests, or a caller-chosen ``chunk``): one workgroup per (context split, KV head,
-  request), then the same merge.
+- ``verify_attention.hip`` (more requests, a caller-chosen ``chunk``, or a single request whose block table holds at
+  most 4096 keys, in 96-key splits): one workgroup per (context split, KV head, request), then the same merge.
 - ``verify_attention_f32.hip``: fp32 rows over fp32 pages (the reference test's dtype).
 
 The cache may be bf16 / fp16, or fp8-e4m3 (OCP) with one fp32 scale per (page, KV head) for keys (``k_scale``) and
@@ -54,8 +54,8 @@ def verify_attention(
     first ``context_lens[b]`` tokens through ``block_table[b]``; ``masks[b, r]`` has bit ``j`` set iff new token
     ``j`` is row ``r`` or one of its ancestors. Every request has at most ``max_query_len`` (<= 64) rows.
     ``k_scale`` / ``v_scale``: fp32 ``[blocks, Hkv]`` scales of an fp8-e4m3 cache. ``chunk``: context keys per split
-    of the split-context schedule (a multiple of 64; 0 lets the library choose the streamed schedule where it
-    applies). ``no_alloc``: allocate nothing; the split partials go to the
+    of the split-context schedule (a multiple of 32; 0 lets the library choose: the streamed schedule where it applies,
+    the split one for a single short request). ``no_alloc``: allocate nothing; the split partials go to the
     library's static per-GPU buffer (``eagle4_verify_attention_static``, 64 MiB), and a launch needing more raises
     ValueError before anything runs. Every such call on one GPU shares that buffer: calls overlapping in time race.
     """
