@@ -704,8 +704,8 @@ def main() -> int:
     EAGER = args.eager
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: the verify path needs no collective and this build runs on a single MI355X "
-              "(--gpus 1). Sharding is described in DESIGN.md.", file=sys.stderr)
+        print("bench.py measures one GPU (--gpus 1): the verify path needs no collective; a sharded deployment runs "
+              "one such process per GPU on its share of the requests and heads.", file=sys.stderr)
         return 2
     import torch
 
