@@ -265,14 +265,43 @@ def library() -> ctypes.CDLL:
     return lib
 
 
+TARGET_ISA = "gfx950"
+
+
+class UnsupportedHardware(RuntimeError):
+    """The device cannot run the library's code objects (they are built for gfx950 only)."""
+
+
+@functools.lru_cache(maxsize=None)
+def _isa_of(index: int) -> tuple[str, str]:
+    props = torch.cuda.get_device_properties(index)
+    if torch.version.hip is None:
+        return props.name, f"sm_{props.major}{props.minor}"
+    return props.name, str(props.gcnArchName).partition(":")[0]
+
+
+def unsupported_reason(device: torch.device) -> Optional[str]:
+    """Why the kernels cannot run on ``device``, in one line; None when they can. A device is covered exactly when
+    the ISA part of its target name (``gfx950`` of ``gfx950:sramecc+:xnack-``) is gfx950."""
+    if device.type != "cuda":
+        return f"tensors are on {device}, not on a ROCm GPU"
+    if not torch.cuda.is_available():
+        return "torch sees no ROCm GPU"
+    name, isa = _isa_of(device.index if device.index is not None else torch.cuda.current_device())
+    if isa != TARGET_ISA:
+        return f"{name} is {isa or 'an unknown ISA'}, and libeagle4_amd.so holds {TARGET_ISA} (MI355X) code objects only"
+    return None
+
+
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
 def launch(name: str, args: ctypes.Structure, device: torch.device) -> None:
     """Calls entry ``name`` on the current stream of ``device``; raises on anything but success."""
-    if device.type != "cuda":
-        raise RuntimeError(f"eagle4_amd: {name} needs tensors on a ROCm GPU, got {device}")
+    reason = unsupported_reason(device)
+    if reason is not None:
+        raise UnsupportedHardware(f"eagle4_amd: {name} cannot run: {reason}")
     fn = getattr(library(), name)
     with torch.cuda.device(device):
         status = fn(ctypes.byref(args), ctypes.c_void_p(stream_of(device)))

@@ -1,19 +1,25 @@
-"""The GDN layer's tree-verify front (``TreeVerify.forward_spec_rows``, vllm/gdn_tree_verify.py:55-106) and the
-accepted-path commit of the linear-attention state (vllm/gdn_tree_verify.py:184-322) for vLLM hybrid targets,
-engine-free.
+"""The linear-attention layer hook of vLLM hybrid targets (vllm/gdn_tree_verify.py): the GDN and Mamba2 layers'
+tree-verify front (``TreeVerify``, :55-148), the checks and factory the speculator and the plugin call
+(``check_tree_verifiable``, ``create_extension``, :151-183) and the accepted-path commit of the layers' states
+(``LinearStateCommit``, :186-322).
 
 vLLM keeps one recurrent-state slot per verify row (``slots[b, i]``) and the request's conv window in slot
 ``slots[b, 0]``; the next step resumes from row / window offset ``num_accepted - 1``. The accepted rows of a tree are
 not a prefix of the verify rows, so :class:`LinearStateCommit` moves them into chain order: the window columns of
 the accepted path next to each other, and the last accepted row's recurrent state into row ``accepted - 1``. All
-layers move in one gfx950 launch per kind (``csrc/state_commit.hip``).
+layers move in one gfx950 launch (``csrc/state_commit.hip``).
+
+With vLLM installed, ``GDNSpecRows`` and the base class of :class:`TreeVerify` are vLLM's (``LinearAttnVerifyExtension``
+through the installed eagle-harness's ``vllm.adapter``), so vLLM can use the extension :func:`create_extension`
+returns; without vLLM they are this module's engine-free stand-ins, with the same fields.
 """
 
 from __future__ import annotations
 
 from collections.abc import Sequence
 from dataclasses import dataclass
-from typing import Any
+from types import ModuleType
+from typing import Any, Optional
 
 import torch
 
@@ -27,26 +33,67 @@ from eagle_harness.vllm.verify_layout import get_stage
 NULL_BLOCK_ID = 0
 
 
-def _caches(layer: Any) -> tuple[torch.Tensor, torch.Tensor]:
-    """(window cache as [slots, dim, state_len], state pool) of a layer: a (conv, ssm) pair or an object with vLLM's
-    ``kv_cache`` = (conv, ssm), conv in either of vLLM's layouts ([slots, dim, len] or [slots, len, dim])."""
-    conv, ssm = layer if isinstance(layer, (tuple, list)) else (layer.kv_cache[0], layer.kv_cache[1])
-    return conv, ssm
+def _vllm_verify_extension() -> Optional[ModuleType]:
+    """vLLM's module of ``LinearAttnVerifyExtension`` and its row types, found by the installed eagle-harness's adapter
+    (vllm/adapter.py:33-41); None when vLLM or the adapter is not installed."""
+    try:
+        from eagle_harness.vllm.adapter import verify_extension_module
+
+        return verify_extension_module()
+    except ModuleNotFoundError as err:
+        if (err.name or "").startswith("vllm") or err.name == "eagle_harness.vllm.adapter":
+            return None
+        raise
+
+
+def _vllm_conv_state_dim_first() -> Optional[bool]:
+    """vLLM's choice of conv-state layout: True for ``[slots, dim, len]``, False for ``[slots, len, dim]``; None
+    without vLLM."""
+    try:
+        from vllm.model_executor.layers.mamba.mamba_utils import is_conv_state_dim_first
+    except ModuleNotFoundError as err:
+        if (err.name or "").startswith("vllm"):
+            return None
+        raise
+    return bool(is_conv_state_dim_first())
+
+
+def _caches(layer: Any, dim_first: Optional[bool]) -> tuple[torch.Tensor, torch.Tensor]:
+    """(window cache viewed as [slots, dim, state_len], state pool) of a layer.
+
+    ``layer`` is either a (window, pool) pair whose window is already a [slots, dim, state_len] view, or a layer
+    object with vLLM's ``kv_cache`` = (conv state, ssm state); the conv state of a layer object is in vLLM's layout,
+    ``[slots, dim, len]`` when ``dim_first`` and ``[slots, len, dim]`` otherwise, and is viewed dim-first (its
+    transpose, no copy), as vllm/gdn_tree_verify.py:261-265 does."""
+    if isinstance(layer, (tuple, list)):
+        conv, ssm = layer
+        return conv, ssm
+    conv, ssm = layer.kv_cache[0], layer.kv_cache[1]
+    if dim_first is None:
+        raise ValueError("LinearStateCommit: the conv-state layout of vLLM layer caches is unknown (vLLM is not "
+                         "installed): pass dim_first=True for [slots, dim, len] caches, False for [slots, len, dim]")
+    return (conv if dim_first else conv.transpose(-1, -2)), ssm
 
 
 class LinearStateCommit:
     """Moves the accepted rows of a tree round into chain order in GDN layers, all layers in one launch.
 
-    ``layers[i]``: layer ``i``'s (window cache viewed as [slots, dim, state_len], state pool [slots, ...]) pair (or a
-    layer object with ``kv_cache``); ``slots[i]``: its KV cache group's [reqs, S] int32 state-slot table.
+    ``layers[i]``: layer ``i``'s (window cache viewed as [slots, dim, state_len], state pool [slots, ...]) pair, or a
+    layer object with vLLM's ``kv_cache`` (conv state, ssm state); ``slots[i]``: its KV cache group's [reqs, S] int32
+    state-slot table. ``dim_first`` gives the conv-state layout of layer objects (``[slots, dim, len]`` when True,
+    ``[slots, len, dim]`` when False); None asks vLLM (``is_conv_state_dim_first``), and layer objects without vLLM
+    and without ``dim_first`` are refused.
     """
 
-    def __init__(self, layers: Sequence[Any], slots: Sequence[torch.Tensor], device: torch.device):
+    def __init__(self, layers: Sequence[Any], slots: Sequence[torch.Tensor], device: torch.device, *,
+                 dim_first: Optional[bool] = None):
         self.num_layers = len(layers)
         self.device = device
         if not self.num_layers:
             return
-        caches = [_caches(layer) for layer in layers]
+        if dim_first is None and not all(isinstance(layer, (tuple, list)) for layer in layers):
+            dim_first = _vllm_conv_state_dim_first()
+        caches = [_caches(layer, dim_first) for layer in layers]
         first_conv, first_ssm = caches[0]
         for conv, ssm in caches:
             if conv.stride() != first_conv.stride() or conv.dtype != first_conv.dtype or ssm.stride() != first_ssm.stride():
@@ -91,35 +138,45 @@ class LinearStateCommit:
         _native.launch("eagle4_linear_state_commit", args, self.device)
 
 
-@dataclass
-class GDNSpecRows:
-    """The speculative-decode rows a Qwen GDN layer hands its verify extension (vLLM's ``GDNSpecRows``, the fields
-    vllm/gdn_tree_verify.py:65-106 reads). ``mixed_qkv`` ``[tokens, 2 H K + HV V]``, ``a`` / ``b`` ``[tokens, HV]``
-    may be token-strided views of the layer's input projection; ``out`` ``[tokens, HV V]`` receives the recurrence
-    output."""
+_VLLM_EXTENSION = _vllm_verify_extension()
 
-    layer_name: str
-    mixed_qkv: torch.Tensor
-    conv_state: torch.Tensor
-    conv_weight: torch.Tensor
-    conv_bias: torch.Tensor | None
-    activation: str | None
-    a: torch.Tensor
-    b: torch.Tensor
-    A_log: torch.Tensor
-    dt_bias: torch.Tensor
-    ssm_state: torch.Tensor
-    state_indices: torch.Tensor
-    query_start_loc: torch.Tensor
-    num_accepted_tokens: torch.Tensor
-    out: torch.Tensor
-    num_k_heads: int
-    head_k_dim: int
-    num_v_heads: int
-    head_v_dim: int
+if _VLLM_EXTENSION is not None:
+    GDNSpecRows = _VLLM_EXTENSION.GDNSpecRows
+    LinearAttnVerifyExtension = _VLLM_EXTENSION.LinearAttnVerifyExtension
+else:
+
+    @dataclass
+    class GDNSpecRows:
+        """The speculative-decode rows a Qwen GDN layer hands its verify extension (vLLM's ``GDNSpecRows``, the fields
+        vllm/gdn_tree_verify.py:65-106 reads). ``mixed_qkv`` ``[tokens, 2 H K + HV V]``, ``a`` / ``b`` ``[tokens, HV]``
+        may be token-strided views of the layer's input projection; ``out`` ``[tokens, HV V]`` receives the recurrence
+        output."""
+
+        layer_name: str
+        mixed_qkv: torch.Tensor
+        conv_state: torch.Tensor
+        conv_weight: torch.Tensor
+        conv_bias: torch.Tensor | None
+        activation: str | None
+        a: torch.Tensor
+        b: torch.Tensor
+        A_log: torch.Tensor
+        dt_bias: torch.Tensor
+        ssm_state: torch.Tensor
+        state_indices: torch.Tensor
+        query_start_loc: torch.Tensor
+        num_accepted_tokens: torch.Tensor
+        out: torch.Tensor
+        num_k_heads: int
+        head_k_dim: int
+        num_v_heads: int
+        head_v_dim: int
+
+    class LinearAttnVerifyExtension:
+        """Engine-free stand-in for vLLM's verify-extension base class (vLLM is not installed)."""
 
 
-class TreeVerify:
+class TreeVerify(LinearAttnVerifyExtension):
     """A GDN layer's tree-verify front (vllm/gdn_tree_verify.py:55-106): the tree conv over the layer's qkv projection,
     then the tree recurrence on q / k / v views of the conv output and a / b views of the projection. No split or copy
     kernel sits between the input projection's GEMM and the conv, nor between the conv and the recurrence: both gfx950
@@ -201,3 +258,32 @@ def _staged() -> Any:
     if stage is None:
         raise RuntimeError("eagle_harness: a linear-attention verify ran before the speculator staged its layout")
     return stage
+
+
+def check_tree_verifiable(layers: Sequence[Any]) -> None:
+    """Refuses a target with linear-attention layers that would not hand their rows to :class:`TreeVerify`
+    (vllm/gdn_tree_verify.py:151-166): vLLM would run its own chain kernels on them and verify every tree as a
+    chain. Qwen GDN layers always hand them over; Mamba2 mixers only where vLLM's extension base class declares the
+    Mamba2 hook (``forward_mamba2_spec_rows``)."""
+    from vllm.model_executor.layers.mamba.gdn.qwen_gdn_linear_attn import QwenGatedDeltaNetAttention
+    from vllm.model_executor.layers.mamba.mamba_mixer2 import MambaMixer2
+
+    served: list[type] = [QwenGatedDeltaNetAttention]
+    if "forward_mamba2_spec_rows" in vars(LinearAttnVerifyExtension):
+        served.append(MambaMixer2)
+    refused = sorted({type(layer).__name__ for layer in layers if not isinstance(layer, tuple(served))})
+    if refused:
+        raise RuntimeError(
+            f"eagle_harness: the tree verify does not reach the {', '.join(refused)} layers of this target with "
+            f"this vLLM: only {', '.join(kind.__name__ for kind in served)} layers pass their rows to the verify "
+            "extension (Mamba2 mixers need vLLM's LinearAttnVerifyExtension.forward_mamba2_spec_rows hook)")
+
+
+def create_extension(vllm_config: Any) -> Optional[TreeVerify]:
+    """The factory vLLM's speculative-method registry calls (``linear_attn_verify_extension``,
+    vllm/gdn_tree_verify.py:176-183): a :class:`TreeVerify` when the method drafts trees, None when it drafts chains
+    (node top-k 1), which vLLM verifies with its own kernels."""
+    from eagle_harness.vllm.config import parse_method_config
+
+    method = parse_method_config(vllm_config.speculative_config.method_config)
+    return None if method.node_top_k == 1 else TreeVerify(vllm_config)

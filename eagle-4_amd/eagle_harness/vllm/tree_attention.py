@@ -1,13 +1,17 @@
-"""The tree path of the target's full-attention backend (vllm/tree_attention.py:29-98), engine-free.
+"""The CUSTOM attention backend of the target's full-attention layers (vllm/tree_attention.py:29-98).
 
 vLLM's ``TreeFlashAttentionImpl`` sends a layer's attention through :func:`verify_attention` when a tree verify is
 staged and leaves every other forward (prefill, one query token per request, the draft's own layers) to
 FlashAttention. Its ``_forward_tree`` splits the layer's cache into K / V views and refuses quantized caches
-(:69-70). This module keeps the same decision and the same call, without the vLLM base classes:
+(:69-70). This module keeps the same decision and the same call:
 
-- :class:`TreeAttentionImpl` takes the plain-path implementation as ``plain`` (any callable with the
-  ``forward`` signature, e.g. the engine's FlashAttention impl); without one, a forward that is not a tree verify
-  raises instead of being computed some other way.
+- with vLLM importable, :class:`TreeFlashAttentionBackend` and :class:`TreeFlashAttentionImpl` derive from vLLM's
+  FlashAttention backend and implementation, as the reference's do, so the plugin's registration string
+  (``eagle_harness.vllm.tree_attention.TreeFlashAttentionBackend``) names a backend vLLM can load, and every forward
+  that is not a tree verify is FlashAttention's own;
+- :class:`TreeAttentionImpl` is the same forward without vLLM: it takes the plain-path implementation as ``plain``
+  (any callable with the ``forward`` signature); without one, a forward that is not a tree verify raises instead of
+  being computed some other way. Without vLLM, :class:`TreeFlashAttentionBackend` serves it;
 - fp8 caches are served instead of refused: a cache of dtype ``float8_e4m3fn`` (or uint8 storage with
   ``kv_cache_dtype`` ``"fp8"`` / ``"fp8_e4m3"``) goes to the kernels with fp32 scales per (page, KV head). They come
   from ``k_scale`` / ``v_scale`` arguments, else from the layer's ``k_page_scale`` / ``v_page_scale`` attributes
@@ -53,14 +57,24 @@ def _page_scales(value: Any, blocks: int, kv_heads: int, device: torch.device, n
     return one.expand(blocks, kv_heads)
 
 
-class TreeAttentionImpl:
-    """``TreeFlashAttentionImpl`` without vLLM (vllm/tree_attention.py:29-88). ``plain`` computes the forwards that
-    are not tree verifies (the reference's ``super().forward``)."""
+def _vllm_flash_attention() -> tuple[Optional[type], Optional[type]]:
+    """vLLM's (FlashAttentionBackend, FlashAttentionImpl); (None, None) when vLLM is not installed."""
+    try:
+        from vllm.v1.attention.backends.flash_attn import FlashAttentionBackend, FlashAttentionImpl
+    except ModuleNotFoundError as err:
+        if not (err.name or "").startswith("vllm"):
+            raise
+        return None, None
+    return FlashAttentionBackend, FlashAttentionImpl
 
-    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
-                 kv_cache_dtype: str = "auto", plain: Optional[Callable[..., torch.Tensor]] = None):
-        self.num_heads, self.head_size, self.scale = num_heads, head_size, scale
-        self.num_kv_heads, self.kv_cache_dtype, self.plain = num_kv_heads, kv_cache_dtype, plain
+
+class _TreeForward:
+    """The backend's forward (vllm/tree_attention.py:29-88): a staged tree verify with more than one query row per
+    request, outside the draft's layers, goes to :func:`verify_attention`; every other forward to
+    :meth:`_plain_forward`. Reads ``head_size``, ``scale`` and ``kv_cache_dtype`` from the implementation."""
+
+    def _plain_forward(self, *args: Any) -> torch.Tensor:
+        raise NotImplementedError
 
     def forward(self, layer: Any, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, kv_cache: torch.Tensor,
                 attn_metadata: Any, output: torch.Tensor, output_scale: Optional[torch.Tensor] = None,
@@ -69,10 +83,8 @@ class TreeAttentionImpl:
         tree = (stage is not None and stage.verifying and attn_metadata is not None
                 and attn_metadata.max_query_len > 1 and not getattr(layer, "is_draft_layer", False))
         if not tree:
-            if self.plain is None:
-                raise _native.NotCovered("not a tree verify forward, and no plain-path implementation was given")
-            return self.plain(layer, query, key, value, kv_cache, attn_metadata, output, output_scale,
-                              output_block_scale)
+            return self._plain_forward(layer, query, key, value, kv_cache, attn_metadata, output, output_scale,
+                                       output_block_scale)
         k_scale = getattr(layer, "k_page_scale", None)
         v_scale = getattr(layer, "v_page_scale", None)
         if k_scale is None and hasattr(layer, "_k_scale"):
@@ -108,14 +120,54 @@ class TreeAttentionImpl:
         return output
 
 
-class TreeFlashAttentionBackend:
-    """The backend name the plugin registers (vllm/tree_attention.py:91-98): ``CUSTOM``, served by
-    :class:`TreeAttentionImpl`."""
+class TreeAttentionImpl(_TreeForward):
+    """The backend's implementation without vLLM. ``plain`` computes the forwards that are not tree verifies (the
+    reference's ``super().forward``)."""
 
-    @staticmethod
-    def get_name() -> str:
-        return "CUSTOM"
+    def __init__(self, num_heads: int, head_size: int, scale: float, num_kv_heads: int,
+                 kv_cache_dtype: str = "auto", plain: Optional[Callable[..., torch.Tensor]] = None):
+        self.num_heads, self.head_size, self.scale = num_heads, head_size, scale
+        self.num_kv_heads, self.kv_cache_dtype, self.plain = num_kv_heads, kv_cache_dtype, plain
 
-    @staticmethod
-    def get_impl_cls() -> type:
-        return TreeAttentionImpl
+    def _plain_forward(self, *args: Any) -> torch.Tensor:
+        if self.plain is None:
+            raise _native.NotCovered("not a tree verify forward, and no plain-path implementation was given")
+        return self.plain(*args)
+
+
+_VllmBackend, _VllmImpl = _vllm_flash_attention()
+
+if _VllmImpl is not None:
+
+    class TreeFlashAttentionImpl(_TreeForward, _VllmImpl):
+        """vLLM's FlashAttention implementation with the tree forward in front of it; vLLM constructs it as it
+        constructs FlashAttention's."""
+
+        def _plain_forward(self, *args: Any) -> torch.Tensor:
+            return _VllmImpl.forward(self, *args)
+
+    class TreeFlashAttentionBackend(_VllmBackend):
+        """vLLM's FlashAttention backend under the name ``CUSTOM``, served by :class:`TreeFlashAttentionImpl`."""
+
+        @staticmethod
+        def get_name() -> str:
+            return "CUSTOM"
+
+        @staticmethod
+        def get_impl_cls() -> type:
+            return TreeFlashAttentionImpl
+
+else:
+    TreeFlashAttentionImpl = TreeAttentionImpl
+
+    class TreeFlashAttentionBackend:
+        """The backend name the plugin registers (vllm/tree_attention.py:91-98): ``CUSTOM``, served by
+        :class:`TreeAttentionImpl` (vLLM is not installed)."""
+
+        @staticmethod
+        def get_name() -> str:
+            return "CUSTOM"
+
+        @staticmethod
+        def get_impl_cls() -> type:
+            return TreeAttentionImpl

@@ -143,6 +143,42 @@ def test_linear_state_commit_matches_oracle(dev, ssm_dtype, layout, conv_dtype, 
         assert torch.equal(gs[layer].cpu(), want_s[layer])
 
 
+@pytest.mark.parametrize("dim_first", [True, False])
+def test_linear_state_commit_from_layer_objects(dev, dim_first):
+    """The speculator builds the commit from vLLM layer objects (``kv_cache`` = [conv state, ssm state]) with the conv
+    state in vLLM's own layout: [slots, dim, len] when dim-first, else [slots, len, dim], which the commit views
+    dim-first (vllm/gdn_tree_verify.py:261-265). Both layouts land bit for bit on the oracle's moves."""
+    from types import SimpleNamespace
+
+    from eagle_harness.vllm.gdn_tree_verify import LinearStateCommit
+
+    announce(f"state commit from layer objects, dim_first={dim_first}")
+    gen = torch.Generator().manual_seed(11)
+    layers, reqs, width, dim = 3, 4, 8, 520
+    slots_n = 1 + reqs * width
+    raw = [torch.randn((slots_n, dim, 2 + width) if dim_first else (slots_n, 2 + width, dim), generator=gen)
+           .to(torch.bfloat16) for _ in range(layers)]
+    ssms = [torch.randn(slots_n, 2, 16, 16, generator=gen) for _ in range(layers)]
+    slots = (1 + torch.arange(reqs * width, dtype=torch.int32)).view(reqs, width)
+    idx = torch.tensor([1, 3, 0, 2], dtype=torch.int32)
+    path = torch.zeros(reqs, width, dtype=torch.int32)
+    plen = torch.ones(reqs, dtype=torch.int32)
+    for s, p in ((0, [0, 2, 5, 7]), (1, [0, 1, 2]), (2, [0, 3, 6]), (3, [0])):
+        path[s, : len(p)] = torch.tensor(p, dtype=torch.int32)
+        plen[s] = len(p)
+    view = (lambda c: c) if dim_first else (lambda c: c.transpose(1, 2))
+    want_c, want_s = [view(c).clone() for c in raw], [s.clone() for s in ssms]
+    ocm.linear_state_commit(want_c, want_s, [slots] * layers, idx, path, plen)
+    objs = [SimpleNamespace(kv_cache=[c.to(dev), s.to(dev)]) for c, s in zip(raw, ssms)]
+    commit = LinearStateCommit(objs, [slots.to(dev)] * layers, dev, dim_first=dim_first)
+    assert commit.dim == dim
+    commit.commit(idx.to(dev), path.to(dev), plen.to(dev))
+    torch.cuda.synchronize()
+    for layer in range(layers):
+        assert torch.equal(view(objs[layer].kv_cache[0]).cpu(), want_c[layer])
+        assert torch.equal(objs[layer].kv_cache[1].cpu(), want_s[layer])
+
+
 def _linked_tree(width, rng):
     """A random tree as first-child / next-sibling links (about half the nodes continue a chain), draft tokens in a
     small vocabulary and a target that follows a child's draft 80 % of the time (the shape of

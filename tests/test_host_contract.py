@@ -135,16 +135,15 @@ def test_greedy_targets_refuses_a_wrong_out():
             greedy_targets(logits, out=out)
 
 
-def test_arch_gate_without_a_gpu():
-    """The device gate on a machine without a ROCm GPU: a reason instead of an exception, every feature off, and
-    require_supported raises UnsupportedHardware."""
-    from eagle_harness.kernels import arch
+def test_device_gate_without_a_gpu():
+    """The launch gate on a machine without a ROCm GPU: a reason instead of an exception, and a launch raises
+    UnsupportedHardware (a RuntimeError) before the library is touched."""
+    from eagle_harness.kernels import _native
 
     if torch.cuda.is_available():
         pytest.skip("a GPU is visible")
-    assert arch.gpu() is None and "no ROCm GPU" in arch.unsupported_reason()
-    assert not any(getattr(arch, name)() for name in arch.FEATURES)
-    with pytest.raises(arch.UnsupportedHardware):
-        arch.require_supported()
-    assert arch.FEATURES["gdn_records_replay"][0] and not arch.FEATURES["pdl"][0]
-    assert arch.pdl.__name__ == "pdl" and "gfx950" in arch.pdl.__doc__
+    assert "not on a ROCm GPU" in _native.unsupported_reason(torch.device("cpu"))
+    assert "no ROCm GPU" in _native.unsupported_reason(torch.device("cuda:0"))
+    with pytest.raises(_native.UnsupportedHardware, match="ROCm GPU"):
+        _native.launch("eagle4_stage_tree", _native.StageTreeArgs(), torch.device("cpu"))
+    assert issubclass(_native.UnsupportedHardware, RuntimeError)
