@@ -1,8 +1,9 @@
 """GDN tree verify: the width-4 causal conv1d of every tree node through the ancestor table
 (kernels/gdn_tree_conv.py).
 
-Each node's window is its three nearest ancestors' inputs (or the request's history columns above the root), read
-through the table :func:`~eagle_harness.kernels.gdn_tree.gdn_tree_ancestors` builds once per forward. Every product
+A node's conv taps are the inputs of the node and of its parent, grandparent and great-grandparent; above the root
+they come from the request's history columns. The table of those three ancestors per node is built once per
+forward (:func:`~eagle_harness.kernels.gdn_tree.gdn_tree_ancestors`). Every product
 is rounded to the 16-bit input dtype before the fp32 accumulation, then SiLU, as the reference's kernels compute it;
 windows and the state roll are copies. One gfx950 kernel serves both engines' layouts (``csrc/gdn_tree_conv.hip``):
 a thread owns 8 adjacent channels of a request and streams its nodes with 16-byte loads and stores.

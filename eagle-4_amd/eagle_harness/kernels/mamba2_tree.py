@@ -1,10 +1,11 @@
 """Mamba2 tree verify (kernels/mamba2_tree.py): the selective state update of every tree node, each continuing from
 its parent, on the gfx950 kernel of ``csrc/mamba2_tree.hip``.
 
-A request's verify rows are tree nodes ordered parent first; row ``t`` of request ``b`` updates the SSM state of its
-parent row (row 0: the request's state) with its own token and stores the result in its own state slot, the layout
-vLLM's chain verify uses. A row whose parent is the previous row continues from the state in registers, any other
-row reloads its parent's stored state, so on a chain this is vLLM's chain step for step.
+The verify rows of a request are its draft-tree nodes, each after its parent. A node takes the SSM state its parent
+left (the root takes the request's own state), applies its token, and stores the new state in the node's own slot:
+one slot per verify row, as vLLM lays out a chain verify. When the parent is the row just before, the state is
+still in registers; otherwise it is read back from the parent's slot. A chain therefore reproduces vLLM's chain
+update exactly.
 """
 
 from __future__ import annotations

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_states_close
 from oracle import accept as oacc
 from oracle import attention as oa
 from oracle import commit as ocm
@@ -156,7 +156,7 @@ def test_gdn_layer_conv_walk_commit(dev, batch):
         retrieve_parent_token=sub["parent_table"], num_accepted_tokens=sub["num_accepted"], pad_slot_id=0)
     _close16(out.cpu()[0, sub["rows"]], o_walk[0])
     snaps = g["pool"][old.flatten().long().to(dev)].cpu()
-    torch.testing.assert_close(snaps, pool[sub["slots"].flatten().long()], atol=1e-5, rtol=1e-4)
+    assert_states_close(snaps, pool[sub["slots"].flatten().long()])
 
     # the commit of every request, checked against its own snapshots and windows taken just before it
     path, plen = accept_paths(g["parents"], seed=batch, width=W)
@@ -182,7 +182,7 @@ def test_gdn_layer_conv_walk_commit(dev, batch):
                             plen[reqs])
     for i, r in enumerate(reqs):
         d_new = int(sub["slots"][i, int(plen[r]) - 1])
-        torch.testing.assert_close(g["pool"][int(dst_state[r])].cpu(), pool[d_new], atol=1e-5, rtol=1e-4)
+        assert_states_close(g["pool"][int(dst_state[r])].cpu(), pool[d_new])
         assert torch.equal(g["conv_state"][int(slots_cpu[r, 0])].cpu(), s_conv[int(sub["slots"][i, 0])])
 
 

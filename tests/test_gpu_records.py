@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_states_close
 from oracle import records as orec
 from oracle import recurrence as orr
 from oracle.tables import _gdn_tree_paths
@@ -314,8 +314,10 @@ def test_commit_matches_oracle_over_layers(dev, pool_dtype, round_state):
     gdn_tree_records_commit(got, records.to(dev), state_indices.to(dev), record_indices.to(dev),
                             commit_steps.to(dev), parent.to(dev), round_state)
     torch.cuda.synchronize()
-    tol = dict(atol=1e-5, rtol=1e-4) if pool_dtype == torch.float32 else dict(atol=1e-2, rtol=1e-2)
-    torch.testing.assert_close(got.cpu().float(), want.float(), **tol)
+    if pool_dtype == torch.float32:
+        assert_states_close(got.cpu(), want)
+    else:
+        torch.testing.assert_close(got.cpu().float(), want.float(), atol=1e-2, rtol=1e-2)
     untouched = [0, 3, 4, 5]  # slots no committed request names
     assert torch.equal(got.cpu()[:, untouched], state[:, untouched])
 
@@ -345,7 +347,7 @@ def test_chunk_then_commit_lands_on_the_walks_accepted_state(dev):
                                   intermediate_state_indices=slots, retrieve_parent_token=inp["parent"],
                                   num_accepted_tokens=torch.tensor([1], dtype=torch.int32), pad_slot_id=0)
     want = snaps[int(slots[0, accepted])]
-    torch.testing.assert_close(pool[0, int(inp["state_indices"][0])].cpu(), want, atol=1e-5, rtol=1e-4)
+    assert_states_close(pool[0, int(inp["state_indices"][0])].cpu(), want)
 
 
 def _per_node_rounded(q, k, v, a, b, A, bias, state, slots, parent, width, batch, hv, h, rounded):

@@ -5,7 +5,7 @@
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, assert_states_close
 from oracle import recurrence as orr
 from workloads import GDN_B1, GdnShape, gdn_inputs, seeded_tree
 
@@ -34,7 +34,7 @@ def _to(d, dev):
 
 
 def _state_close(got, want):
-    torch.testing.assert_close(got.float(), want.float(), atol=1e-5, rtol=1e-4)
+    assert_states_close(got.float(), want.float())
 
 
 def _vllm_case(dev, parent_lists, dims, state_dtype=torch.float32, edit_slots=None, seed=1):
