@@ -801,7 +801,7 @@ def main() -> int:
 
     def run_commit():
         commit.commit(idx, path_d, path_len_d)
-        positions.copy_(chain_pos)  # the next round's chain positions (the stage rewrites them to depths)
+        stage.restore_positions(positions, tokens)  # the chain positions back (the stage rewrote them to depths)
 
     parts = dict(stage=run_stage, attention=run_attention, conv=run_conv, recurrence=run_recurrence,
                  commit=run_commit)
@@ -847,13 +847,20 @@ def main() -> int:
                     commit.commit(idx, path_d, path_len_d)  # the commit part without its positions copy
                 else:
                     parts[n]()
-            positions.copy_(chain_pos)
+            stage.restore_positions(positions, tokens)
         return run
 
     timing = "hip-graph replay"
     try:
         g_step = graph_of(step)
         g_less = {n: graph_of(without(n)) for n in names}
+        # The parts first (each variant replayed back to back against the whole step), then the headline: W
+        # warm-up replays and exactly K timed ones. A GPU coming out of idle runs its first few dozen step replays
+        # up to ~4 % slower while its clocks ramp; measuring the parts first means the K timed steps see the
+        # steady state a serving loop runs in.
+        reps = max(args.steps, 30)
+        t_step = timed(g_step.replay, reps)
+        per = {n: t_step - timed(g_less[n].replay, reps) for n in names}
         for _ in range(args.warmup):
             g_step.replay()
         torch.cuda.synchronize()
@@ -862,9 +869,6 @@ def main() -> int:
             g_step.replay()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        reps = max(args.steps, 30)
-        t_step = timed(g_step.replay, reps)
-        per = {n: t_step - timed(g_less[n].replay, reps) for n in names}
     except RuntimeError as err:  # capture unavailable: eager launches (host time between launches included)
         timing = f"eager ({err.__class__.__name__}: graph capture failed)"
         torch.cuda.synchronize()

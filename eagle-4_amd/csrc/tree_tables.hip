@@ -11,7 +11,15 @@ namespace {
 
 constexpr int kStageMaxWidth = 64;
 
-// vllm/verify_layout.py:31-86 (_stage_tree_kernel).
+// vllm/verify_layout.py:31-86 (_stage_tree_kernel), with VerifyStage.stage's save of the chain positions (:159)
+// folded in: each request's workgroup copies its own rows' positions before rewriting them (and the last one the
+// tokens after the last request), so no separate copy launch runs.
+//
+// Lane u holds row u. A parent-first tree (0 <= parent(u) < u for 0 < u < W: every tree the drafter builds) is
+// staged by pointer jumping over lane shuffles: depths and ancestor-or-self masks accumulate along the jumps (at
+// most six rounds for 64 rows), the window codes are the parent, grandparent and great-grandparent read directly.
+// Anything else replays the reference's serial update order on one lane, so every input stages as the reference
+// stages it.
 __global__ __launch_bounds__(64) void stage_tree_kernel(const eagle4_stage_tree_args a) {
   __shared__ int32_t s_par[kStageMaxWidth], s_depth[kStageMaxWidth];
   __shared__ int32_t s_anc1[kStageMaxWidth], s_anc2[kStageMaxWidth], s_anc3[kStageMaxWidth];
@@ -20,48 +28,93 @@ __global__ __launch_bounds__(64) void stage_tree_kernel(const eagle4_stage_tree_
   const int lane = threadIdx.x;
   const int W = a.width;
   const int WP = W <= 1 ? 1 : (1 << (32 - __clz(W - 1)));
+  // one round of independent table loads, then the request's parents and positions together
   const int64_t slot = e4::ld(a.idx_mapping, b);
   const int64_t start = e4::ld(a.query_start_loc, b);
   const int64_t width = e4::ld(a.query_start_loc, b + 1) - start;
-  const bool is_tree = a.tree && width > 1 &&
-                       width == e4::ld(a.cu_num_logits, b + 1) - e4::ld(a.cu_num_logits, b);  // :54
-  const int64_t pos0 = a.positions[start];
-  if (lane < WP) {
-    const int32_t loaded = lane < W ? static_cast<int32_t>(e4::ld(a.parents, slot, lane)) : -1;  // :57
-    s_par[lane] = is_tree ? loaded : lane - 1;                                                   // :59
-    s_depth[lane] = 0;
-    s_anc1[lane] = -1;
-    s_anc2[lane] = -2;
-    s_anc3[lane] = -3;
-    s_mask[lane] = 1;
-  }
-  __syncthreads();
-  if (lane == 0) {
-    // :66-74 in the kernel's update order; a parent outside [0, WP) reads zeros, like the masked vector sums
-    for (int r = 1; r < W; ++r) {
-      const int p = s_par[r];
-      const bool in = p >= 0 && p < WP;
-      s_depth[r] = (in ? s_depth[p] : 0) + 1;
-      s_anc1[r] = p;
-      s_anc2[r] = in ? s_anc1[p] : 0;
-      s_anc3[r] = in ? s_anc2[p] : 0;
-      s_mask[r] = (in ? s_mask[p] : 0) | (static_cast<int64_t>(1) << r);
+  const int64_t logits = e4::ld(a.cu_num_logits, b + 1) - e4::ld(a.cu_num_logits, b);
+  const bool is_tree = a.tree && width > 1 && width == logits;  // :54
+  const int32_t loaded = lane < W ? static_cast<int32_t>(e4::ld(a.parents, slot, lane)) : -1;  // :57
+  const int64_t pos = lane < width ? a.positions[start + lane] : 0;
+  const int64_t pos0 = width > 0 ? __shfl(pos, 0, 64) : a.positions[start];  // :52 reads it for any width
+  if (a.chain_positions != nullptr) {  // the saved chain positions: this request's rows, before the rewrite below
+    if (lane < width) a.chain_positions[start + lane] = pos;
+    for (int64_t i = start + 64 + lane; i < start + width; i += 64) a.chain_positions[i] = a.positions[i];
+    if (b == 0) {  // the tokens before the first request
+      for (int64_t i = lane; i < start; i += 64) a.chain_positions[i] = a.positions[i];
+    }
+    if (b == a.num_reqs - 1) {  // the tokens after the last request
+      for (int64_t i = start + width + lane; i < a.num_tokens; i += 64) a.chain_positions[i] = a.positions[i];
     }
   }
-  __syncthreads();
+  const int par = is_tree ? loaded : lane - 1;  // :59 (lanes past W: -1 from the load, or a chain's lane - 1)
+  const bool parent_first = __ballot(lane > 0 && lane < W && (par < 0 || par >= lane)) == 0;
+  int depth = 0, anc1 = -1, anc2 = -2, anc3 = -3;
+  int64_t mask = 1;
+  if (parent_first) {
+    const bool row = lane > 0 && lane < W;
+    int up = row ? par : lane;                    // the root and lanes past W point at themselves
+    depth = row ? 1 : 0;
+    // every row descends from the root: its bit 0 is set from the start (a jump that reaches the root stops the
+    // loop before the root's own mask would be read)
+    mask = row ? ((static_cast<int64_t>(1) << lane) | 1) : (lane == 0 ? 1 : 0);
+    for (int r = 0; r < 6 && __ballot(row && up != 0) != 0; ++r) {
+      const int d2 = __shfl(depth, up, 64);
+      const int64_t m2 = __shfl(mask, up, 64);
+      const int u2 = __shfl(up, up, 64);
+      depth += d2;
+      mask |= m2;
+      up = u2;
+    }
+    const int p1 = __shfl(par, row ? par : 0, 64);  // the parent's parent (row 0's -1 for a child of the root)
+    const int p2 = __shfl(par, row && p1 > 0 ? p1 : 0, 64);
+    if (row) {
+      anc1 = par;
+      anc2 = par == 0 ? -1 : p1;            // anc1 of the parent: the root's is -1
+      anc3 = par == 0 ? -2 : (p1 == 0 ? -1 : p2);  // anc2 of the parent
+    }
+  } else {
+    if (lane < WP) {
+      s_par[lane] = par;
+      s_depth[lane] = 0;
+      s_anc1[lane] = -1;
+      s_anc2[lane] = -2;
+      s_anc3[lane] = -3;
+      s_mask[lane] = 1;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      // :66-74 in the kernel's update order; a parent outside [0, WP) reads zeros, like the masked vector sums
+      for (int r = 1; r < W; ++r) {
+        const int p = s_par[r];
+        const bool in = p >= 0 && p < WP;
+        s_depth[r] = (in ? s_depth[p] : 0) + 1;
+        s_anc1[r] = p;
+        s_anc2[r] = in ? s_anc1[p] : 0;
+        s_anc3[r] = in ? s_anc2[p] : 0;
+        s_mask[r] = (in ? s_mask[p] : 0) | (static_cast<int64_t>(1) << r);
+      }
+    }
+    __syncthreads();
+    if (lane < W) {
+      depth = s_depth[lane];
+      anc1 = s_anc1[lane];
+      anc2 = s_anc2[lane];
+      anc3 = s_anc3[lane];
+      mask = s_mask[lane];
+    }
+  }
   if (lane == 0) a.context_lens[b] = static_cast<int32_t>(pos0);  // :52
   if (lane < W) {
     const int64_t out = static_cast<int64_t>(b) * W + lane;
-    a.stage_parents[out] = s_par[lane];
-    a.stage_anc[static_cast<int64_t>(b) * 3 * W + lane] = s_anc1[lane];
-    a.stage_anc[static_cast<int64_t>(b) * 3 * W + W + lane] = s_anc2[lane];
-    a.stage_anc[static_cast<int64_t>(b) * 3 * W + 2 * W + lane] = s_anc3[lane];
-    a.stage_mask[out] = s_mask[lane];
-    a.slot_parents[slot * W + lane] = s_par[lane];
-    a.slot_depths[slot * W + lane] = s_depth[lane];
-    if (is_tree && lane < width) {  // :85-86: chain position = context + row; tree position = context + depth
-      a.positions[start + lane] = a.positions[start + lane] - lane + s_depth[lane];
-    }
+    a.stage_parents[out] = par;
+    a.stage_anc[static_cast<int64_t>(b) * 3 * W + lane] = anc1;
+    a.stage_anc[static_cast<int64_t>(b) * 3 * W + W + lane] = anc2;
+    a.stage_anc[static_cast<int64_t>(b) * 3 * W + 2 * W + lane] = anc3;
+    a.stage_mask[out] = mask;
+    a.slot_parents[slot * W + lane] = par;
+    a.slot_depths[slot * W + lane] = depth;
+    if (is_tree && lane < width) a.positions[start + lane] = pos - lane + depth;  // :85-86: context + depth
   }
 }
 

@@ -5,7 +5,9 @@
 // draft tiles — in request order. A persistent grid of one workgroup per resident slot takes equal contiguous shares
 // of that sequence, so every CU streams the same number of KV bytes whatever the context lengths are, and no
 // workgroup drains its pipeline between segments. A segment that lies inside one share is normalised and written
-// directly; one cut by share boundaries leaves fp32 partials (with their log2-sum-exp) that a second kernel merges.
+// directly; one cut by share boundaries leaves fp32 partials (with their log2-sum-exp), at most two per share (its
+// first and its last piece), in slots numbered by the share, so the workspace is bounded by the grid whatever the
+// batch; a second kernel merges them.
 //
 // A workgroup is C consumer waves, each owning 16 query rows (a row is a (draft token, query head of the KV head's
 // group) pair, so one read of a K / V tile serves all G W rows), and two producer waves. The producers run the page
@@ -796,7 +798,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
           store_rows<D, T>(static_cast<uint16_t*>(a.out) + (cc.qs + t) * a.stride_ot + head * a.stride_oh, acc, inv,
                            g);
         } else {
-          const int64_t part = (static_cast<int64_t>(cc.b) * HR + cc.k + w) * rows_seg + 16 * wave + l16;
+          // slot 2 w: the share's first piece (it starts inside a segment); 2 w + 1: its last (it ends inside one)
+          const int64_t part = (piece_j0 > 0 ? 2 * w : 2 * w + 1) * static_cast<int64_t>(rows_seg) + 16 * wave + l16;
           store_partial<D>(a.workspace + p.part_off + part * D, acc, inv, g);
           if (g == 0) a.workspace[p.lse_off + part] = ls > 0.f ? mref + log2f(ls) : -INFINITY;
         }
@@ -840,6 +843,7 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
   const int64_t tiles_all = pre[a.num_reqs] * p.HR;
   const int64_t nact = active_groups(tiles_all, p.nwg);
   const int64_t start = pre[b] * p.HR + k * tiles, end = start + tiles;
+  // the shares holding the segment's first and last tiles (share w covers [floor(T w / n), floor(T (w + 1) / n)))
   const int64_t w0 = ((start + 1) * nact - 1) / tiles_all, w1 = (end * nact - 1) / tiles_all;
   if (w0 == w1) return;  // inside one share: written directly
   const int item = blockIdx.y * 256 + threadIdx.x;
@@ -864,7 +868,9 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
 #pragma unroll
     for (int i = 0; i < kGroup; ++i) {
       const bool in = wg + i <= w1;
-      const int64_t part = (s + wg + i) * rows_seg + r;
+      // share w0's piece is its last (slot 2 w0 + 1), every later share's its first (slot 2 w)
+      const int64_t piece = in ? wg + i : w0;
+      const int64_t part = (piece == w0 ? 2 * piece + 1 : 2 * piece) * rows_seg + r;
       ls[i] = in ? a.workspace[p.lse_off + part] : -INFINITY;
 #pragma unroll
       for (int c = 0; c < NV; ++c)
@@ -995,15 +1001,15 @@ bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
     return resident_groups<K::D, K::C, typename K::T, K::FP8>();
   });
   if (p.nwg <= 0) return false;
-  const int64_t slots = static_cast<int64_t>(a.num_reqs) * p.HR + p.nwg;
+  const int64_t slots = 2 * static_cast<int64_t>(p.nwg);  // a share's first and last piece
   const int64_t rows_seg = p.rows_seg;
   p.part_off = (2 * (static_cast<int64_t>(a.num_reqs) + 1) + 63) / 64 * 64;
   p.lse_off = p.part_off + slots * rows_seg * a.D;
   return true;
 }
 
-int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args& a) {
-  const int64_t slots = static_cast<int64_t>(a.num_reqs) * p.HR + p.nwg;
+int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args&) {
+  const int64_t slots = 2 * static_cast<int64_t>(p.nwg);
   return (p.lse_off + slots * p.rows_seg) * static_cast<int64_t>(sizeof(float));
 }
 

@@ -84,7 +84,8 @@ def _fields(spec: str) -> list:
 class StageTreeArgs(ctypes.Structure):
     _fields_ = _fields(
         "parents:t idx_mapping:t query_start_loc:t cu_num_logits:t positions:p stage_parents:p stage_anc:p "
-        "stage_mask:p context_lens:p slot_parents:p slot_depths:p num_reqs:i width:i tree:i reserved:i"
+        "stage_mask:p context_lens:p slot_parents:p slot_depths:p chain_positions:p num_reqs:i width:i tree:i "
+        "num_tokens:i"
     )
 
 
@@ -235,7 +236,7 @@ ENTRIES = {
     "eagle4_mamba2_tree_state_update": (Mamba2Args, 16),
 }
 EXTRA_SYMBOLS = ("eagle4_verify_attention_workspace", "eagle4_verify_attention_static_bytes", "eagle4_version",
-                 "eagle4_args_size")
+                 "eagle4_args_size", "eagle4_init")
 
 
 @functools.lru_cache(maxsize=None)
@@ -262,6 +263,12 @@ def library() -> ctypes.CDLL:
     lib.eagle4_verify_attention_workspace.restype = ctypes.c_int64
     lib.eagle4_verify_attention_static_bytes.argtypes = []
     lib.eagle4_verify_attention_static_bytes.restype = ctypes.c_int64
+    lib.eagle4_init.argtypes = []
+    lib.eagle4_init.restype = ctypes.c_int
+    if torch.cuda.is_available():  # the static arrays' device addresses, looked up now rather than on a first call
+        status = lib.eagle4_init()
+        if status != OK:
+            raise RuntimeError(f"eagle4_amd: eagle4_init failed with HIP error {status}")
     return lib
 
 
@@ -312,3 +319,9 @@ def launch(name: str, args: ctypes.Structure, device: torch.device) -> None:
                          f"({library().eagle4_verify_attention_static_bytes()} bytes); nothing was launched")
     if status != OK:
         raise RuntimeError(f"eagle4_amd: {name} failed with HIP error {status}")
+
+
+# On a GPU machine the library is loaded (and its static arrays' device addresses looked up, eagle4_init) when this
+# binding is imported, so that set-up never happens inside a caller's graph capture.
+if torch.cuda.is_available() and Path(os.environ.get("EAGLE4_AMD_LIB", LIBRARY)).exists():
+    library()

@@ -36,10 +36,13 @@ def stage_tree(
     num_reqs: int,
     *,
     tree: bool,
+    chain_positions: torch.Tensor | None = None,
+    num_tokens: int = 0,
 ) -> None:
     """The engine-free form of ``_stage_tree_kernel`` (vllm/verify_layout.py:31-86): per request, depth, the three
     window codes, the ancestor-or-self int64 mask, ``context_lens = positions[start]`` and, for a tree, positions
-    rewritten to ``context + depth``; chains for anything that is not a tree."""
+    rewritten to ``context + depth``; chains for anything that is not a tree. With ``chain_positions``, the same
+    launch first saves ``positions[:num_tokens]`` into it (VerifyStage.stage's copy, :159)."""
     width = stage_parents.shape[1]
     if width > 64:
         raise ValueError(f"a verify tree has at most 64 rows, got {width}")
@@ -47,6 +50,9 @@ def stage_tree(
                     (slot_parents, "slot_parents"), (slot_depths, "slot_depths")):
         assert t.is_contiguous(), f"{name} must be contiguous"
     assert positions.dtype == torch.int64 and stage_mask.dtype == torch.int64
+    if chain_positions is not None:
+        assert chain_positions.dtype == torch.int64 and chain_positions.is_contiguous()
+        assert chain_positions.numel() >= num_tokens and positions.numel() >= num_tokens
     args = _native.StageTreeArgs(
         parents=_native.itab(parents),
         idx_mapping=_native.itab(idx_mapping),
@@ -59,9 +65,11 @@ def stage_tree(
         context_lens=context_lens.data_ptr(),
         slot_parents=slot_parents.data_ptr(),
         slot_depths=slot_depths.data_ptr(),
+        chain_positions=_native.ptr(chain_positions),
         num_reqs=num_reqs,
         width=width,
         tree=int(tree),
+        num_tokens=num_tokens if chain_positions is not None else 0,
     )
     _native.launch("eagle4_stage_tree", args, positions.device)
 
@@ -129,7 +137,6 @@ class VerifyStage:
         :meth:`restore_positions`. With ``tree=False`` every request is staged as a chain and ``positions`` keep
         their values. ``model_positions``, when the model reads positions from a separate (e.g. multi-row)
         tensor, is shifted by the same per-token amounts."""
-        self.chain_positions[:num_tokens].copy_(positions[:num_tokens])
         stage_tree(
             store.parents,
             idx_mapping,
@@ -144,6 +151,8 @@ class VerifyStage:
             self.slot_depths,
             num_reqs,
             tree=tree,
+            chain_positions=self.chain_positions,
+            num_tokens=num_tokens,
         )
         self.active = tree
         if model_positions is not None:

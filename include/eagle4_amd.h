@@ -64,10 +64,12 @@ typedef struct eagle4_stage_tree_args {
   int32_t* context_lens;       /* [R] */
   int32_t* slot_parents;       /* [slots, W] contiguous */
   int32_t* slot_depths;        /* [slots, W] contiguous */
+  int64_t* chain_positions;    /* optional [tokens]: receives positions[:num_tokens] as they were before the rewrite
+                                  (VerifyStage.stage's save, vllm/verify_layout.py:159, in the same launch) */
   int32_t num_reqs;
   int32_t width; /* W <= 64 */
   int32_t tree;  /* 0: stage every request as a chain */
-  int32_t reserved;
+  int32_t num_tokens; /* tokens of positions saved into chain_positions */
 } eagle4_stage_tree_args;
 int eagle4_stage_tree(const eagle4_stage_tree_args* args, void* stream);
 
@@ -404,6 +406,10 @@ int eagle4_row_attention(const eagle4_row_attn_args* args, void* stream);
 
 /* ---- library introspection ---------------------------------------------------------------------------------------- */
 const char* eagle4_version(void);
+/* Looks up, on the current GPU, the device address of the allocation-free attention's static scratch, so that entry
+ * point does not have to on its first call there (e.g. under graph capture). Optional; returns 0 or a hipError_t. No
+ * counterpart in the reference. */
+int eagle4_init(void);
 /* sizeof() of argument struct `which` (0 stage, 1 ancestors, 2 tail words, 3 conv, 4 gdn, 5 records, 6 records commit,
  * 7 attention, 8 argmax, 9 accept tree, 10 accept tail, 11 compact rows, 12 state commit, 13 compact kv,
  * 14 chainize, 15 row attention, 16 mamba2); -1 past the end. The host binding checks its struct mirrors against these. */

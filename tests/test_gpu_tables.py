@@ -21,7 +21,9 @@ def _random_parents(width, seed):
 
 
 @pytest.mark.parametrize(
-    "parents", [PARENTS, _random_parents(16, 1), _random_parents(16, 2), _random_parents(64, 3), [-1, 0, 1, 2, 3]]
+    "parents", [PARENTS, _random_parents(16, 1), _random_parents(16, 2), _random_parents(64, 3), [-1, 0, 1, 2, 3],
+                # not parent first (a forward parent, one past the row range, a negative one): the serial update order
+                [-1, 3, 0, 1, 9, 2, -5]]
 )
 @pytest.mark.parametrize("tree", [True, False])
 def test_stage_matches_oracle(dev, parents, tree):
@@ -63,6 +65,8 @@ def test_stage_matches_oracle(dev, parents, tree):
         assert stage.slot_parents[s].cpu().tolist() == want["slot_parents"][s].tolist()
         assert stage.slot_depths[s].cpu().tolist() == want["slot_depths"][s].tolist()
     assert pos_d.cpu().numpy().tolist() == pos.tolist()
+    # the same launch saved the chain positions the stage rewrote
+    assert stage.chain_positions[: int(qsl[-1])].cpu().tolist() == positions.tolist()
 
 
 def _links_case(widths, seed, pad_rows=()):
