@@ -193,3 +193,18 @@ def test_mamba2_layer_front_views(dev):
                                                        for k, v in kw.items()})
     torch.testing.assert_close(out2.cpu().float(), o_want.float(), atol=2e-2, rtol=1e-2)
     torch.testing.assert_close(ssm2.cpu(), s_want, atol=1e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("shape,bs", [("tp1", 10), ("super-tp4", 40)])
+def test_nontemporal_state_stores(dev, shape, bs):
+    """Launches whose stored states exceed the 256 MB last-level cache (320 MB here: 10 requests x 16 nodes at Nano
+    TP1 in fp32, 40 requests at Super TP4 with a bf16 pool) store them with the nontemporal buffer-store path.
+    Random 16-node trees, accepted counts, and one request with a pad slot mid-tree, which keeps the index-order walk:
+    its nodes reload parent states that were stored nontemporally in the same launch. The bf16 pool is held to the
+    reference test's 16-bit tolerances (a state's last bit can round either way where the fp32 arithmetic differs in
+    its last bit, and 640 trees carry such flips on); the fp32 pool to the fp32 ones."""
+    announce(f"mamba2 nontemporal state stores {shape} bs={bs}")
+    rng = random.Random(81 + bs)
+    trees = [_tree("random", 16, rng) for _ in range(bs)]
+    accepted = [1 + rng.randrange(4) for _ in range(bs)]
+    _case(dev, shape, trees, 81, pads=[(1, 7)], accepted=accepted, ref_tol=SHAPES[shape][4] != torch.float32)
