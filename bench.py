@@ -581,20 +581,25 @@ def _configs(steps: int) -> dict:
 
 
 def _cpu_configs(seconds: float) -> dict:
-    """The oracle (torch on this host's cores) over configurations 1-4: attention fp32 at batch 1, the GDN layer
-    (conv, walk, commit) at batch 1, bf16 attention at batch 64, the GDN layer at batch 256. The batch-64 and -256
-    configurations run on a sample of 8 and 16 requests of their shape (the oracle's cost is linear in requests, so
-    tokens/s carries over). Each is timed in whole passes for at least ``seconds`` (one pass at least)."""
+    """The oracle (torch on this host's cores) over the configurations, each timed in whole passes for at least
+    ``seconds`` (one pass at least, after an untimed one): configurations 1-4 whole (attention fp32 at batch 1, the
+    GDN layer with conv, walk and commit at batch 1, bf16 attention at batch 64, the GDN layer at batch 256), and
+    configuration 5, the quantized hybrid round at batch 512, layer by layer on a sample of 32 of its requests (fp8
+    attention, three GDN layers through one reused state pool, greedy targets over 151936 tokens, the walk, the commit
+    of the three layers), its tokens/s extrapolated linearly (the oracle's cost is linear in requests; the whole
+    round's 3 x 17 GB of snapshots and 2.5 GB of logits are left out)."""
     import dataclasses
     import platform
 
     import torch
 
+    from oracle import accept as oacc
     from oracle import attention as oa
     from oracle import commit as ocm
     from oracle import conv as oc
     from oracle import recurrence as orr
-    from workloads import ATTN_B1, ATTN_B64, GDN_B1, GDN_B256, accept_paths, attention_inputs, gdn_inputs
+    from workloads import (ATTN_B1, ATTN_B64, ATTN_B512_FP8, GDN_B1, GDN_B256, GdnShape, accept_paths,
+                           attention_inputs, gdn_inputs)
 
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
@@ -614,30 +619,18 @@ def _cpu_configs(seconds: float) -> dict:
             passes += 1
         return (time.perf_counter() - t0) / passes
 
-    out = {"cores": threads, "cpu_model": model, "kind": "port"}
-    for name, shape, dtype in (("cfg1_attention_fp32_b1", ATTN_B1, torch.float32),
-                               ("cfg3_attention_bf16_b64", dataclasses.replace(ATTN_B64, batch=8), torch.bfloat16)):
-        a = attention_inputs(shape, seed=0, dtype=dtype)
+    def attention_pass(a, width, **kw):
+        return lambda: oa.verify_attention(a["q"], a["k_new"], a["v_new"], a["key_cache"], a["value_cache"],
+                                           a["block_table"], a["context_lens"], a["query_start_loc"], a["masks"],
+                                           a["scale"], torch.empty_like(a["q"]), max_query_len=width, **kw)
 
-        def attn():
-            oa.verify_attention(a["q"], a["k_new"], a["v_new"], a["key_cache"], a["value_cache"], a["block_table"],
-                                a["context_lens"], a["query_start_loc"], a["masks"], a["scale"],
-                                torch.empty_like(a["q"]), max_query_len=shape.width)
-
-        s = timed(attn)
-        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch,
-                     "verified_tree_tokens_per_s": shape.batch * shape.width / s}
-        del a
-    for name, shape in (("cfg2_gdn_layer_b1", GDN_B1), ("cfg4_gdn_layer_b256", dataclasses.replace(GDN_B256, batch=16))):
-        g = gdn_inputs(shape, seed=0, layout="vllm")
-        path, plen = accept_paths(g["parents"], 0, shape.width)
+    def gdn_pass(g, shape, path, plen):
+        """Conv, walk and commit of one layer. Passes after the first start from the states the commit left (the
+        cost of a pass does not depend on them)."""
         tokens, HK = shape.batch * shape.width, shape.h * shape.k
         slots0 = g["slots"][:, 0].contiguous()
-        pool0, conv0 = g["pool"].clone(), g["conv_state"].clone()
 
-        def gdn_layer():
-            g["pool"].copy_(pool0)
-            g["conv_state"].copy_(conv0)
+        def run():
             conv_out = torch.empty_like(g["x"])
             oc.gdn_tree_conv1d_update(g["x"].t()[None], g["conv_state"], g["conv_weight"], None, "silu", slots0, None,
                                       None, g["ancestors"], pad_slot_id=0, out=conv_out.t()[None],
@@ -653,10 +646,55 @@ def _cpu_configs(seconds: float) -> dict:
             ocm.linear_state_commit([g["conv_state"]], [g["pool"]], [g["slots"]],
                                     torch.arange(shape.batch, dtype=torch.int32), path, plen)
 
-        s = timed(gdn_layer)
-        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch, "verified_tree_tokens_per_s": tokens / s,
-                     "note": "the pass restores the state pool and conv state first (two host copies)"}
-        del g, pool0, conv0
+        return run
+
+    out = {"cores": threads, "cpu_model": model, "kind": "port"}
+    for name, shape, dtype in (("cfg1_attention_fp32_b1", ATTN_B1, torch.float32),
+                               ("cfg3_attention_bf16_b64", ATTN_B64, torch.bfloat16)):
+        a = attention_inputs(shape, seed=0, dtype=dtype)
+        s = timed(attention_pass(a, shape.width))
+        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch,
+                     "verified_tree_tokens_per_s": shape.batch * shape.width / s}
+        del a
+    for name, shape in (("cfg2_gdn_layer_b1", GDN_B1), ("cfg4_gdn_layer_b256", GDN_B256)):
+        g = gdn_inputs(shape, seed=0, layout="vllm")
+        path, plen = accept_paths(g["parents"], 0, shape.width)
+        s = timed(gdn_pass(g, shape, path, plen))
+        out[name] = {"ms_per_pass": s * 1e3, "requests": shape.batch,
+                     "verified_tree_tokens_per_s": shape.batch * shape.width / s}
+        del g
+
+    # configuration 5 on a sample of its requests, layer by layer
+    sample, B5, vocab = 32, ATTN_B512_FP8.batch, 151936
+    shape_a = dataclasses.replace(ATTN_B512_FP8, batch=sample)
+    shape_g = GdnShape(sample, 16, 16, 32, 128, 128)
+    W = shape_a.width
+    a = attention_inputs(shape_a, seed=9, fp8=True)
+    g = gdn_inputs(shape_g, seed=9, layout="vllm")  # one state pool, reused by the three layers
+    path, plen = accept_paths(g["parents"], 9, W)
+    gen = torch.Generator().manual_seed(9)
+    logits = torch.randn(sample * W, vocab, generator=gen).bfloat16()
+    drafted = torch.randint(0, vocab, (sample * W,), generator=gen)
+    cu = torch.arange(0, sample * W + 1, W, dtype=torch.int32)
+    idx = torch.arange(sample, dtype=torch.int32)
+    parents = torch.tensor(a["parents"], dtype=torch.int32)
+    attn = attention_pass(a, W, k_scale=a["k_scale"], v_scale=a["v_scale"])
+    layer = gdn_pass(g, shape_g, path, plen)
+
+    def round5():
+        attn()
+        for _ in range(3):
+            layer()
+        target = oacc.argmax_rows(logits)
+        oacc.accept_tree(target, drafted, cu, idx, parents, torch.zeros(sample, W, dtype=torch.int32),
+                         torch.ones(sample, dtype=torch.int32), W)
+
+    s = timed(round5)
+    out["cfg5_hybrid_round_b512"] = {
+        "ms_per_pass": s * 1e3, "requests": sample, "of_requests": B5,
+        "verified_tree_tokens_per_s": sample * W / s,
+        "sample": f"{sample} of {B5} requests, the round's parts layer by layer (three GDN layers through one state "
+                  "pool); tokens/s extrapolated linearly in requests"}
     return out
 
 
@@ -694,8 +732,8 @@ def main() -> int:
     ap.add_argument("--step-only", action="store_true",
                     help="time only the verify step (no records chunk, rows or configurations); for quick comparisons")
     ap.add_argument("--configs-only", action="store_true", help="time only the configuration rounds and print them")
-    ap.add_argument("--cpu-configs", type=float, default=2.0,
-                    help="seconds per configuration for the oracle's CPU times of configurations 1-4 (0: skip)")
+    ap.add_argument("--cpu-configs", type=float, default=0.5,
+                    help="seconds per configuration for the oracle's CPU times of configurations 1-5 (negative: skip)")
     ap.add_argument("--eager", action="store_true",
                     help="rows, records and configurations without graph capture (for counter runs); times include "
                          "launch gaps")
@@ -855,10 +893,12 @@ def main() -> int:
         g_step = graph_of(step)
         g_less = {n: graph_of(without(n)) for n in names}
         # The parts first (each variant replayed back to back against the whole step), then the headline: W
-        # warm-up replays and exactly K timed ones. A GPU coming out of idle runs its first few dozen step replays
-        # up to ~4 % slower while its clocks ramp; measuring the parts first means the K timed steps see the
-        # steady state a serving loop runs in.
+        # warm-up replays and exactly K timed ones. A GPU coming out of idle runs its first hundred or so step
+        # replays up to ~5 % slower while its clocks ramp: the parts are timed after 100 untimed replays, and the
+        # K timed steps come after them, in the steady state a serving loop runs in.
         reps = max(args.steps, 30)
+        for _ in range(100):
+            g_step.replay()
         t_step = timed(g_step.replay, reps)
         per = {n: t_step - timed(g_less[n].replay, reps) for n in names}
         for _ in range(args.warmup):
@@ -924,8 +964,9 @@ def main() -> int:
         print("[bench] rows timed", file=sys.stderr, flush=True)
         result["configs"] = _configs(args.steps)
         print("[bench] configuration rounds timed", file=sys.stderr, flush=True)
-        if args.cpu_configs > 0:
+        if args.cpu_configs >= 0:
             result["cpu_configs"] = _cpu_configs(args.cpu_configs)
+            print("[bench] CPU configurations timed", file=sys.stderr, flush=True)
     print(json.dumps(result), flush=True)
     return 0
 
