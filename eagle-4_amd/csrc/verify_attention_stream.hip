@@ -209,7 +209,7 @@ E4_DEV uint2 lds_tr8(uint32_t addr) {
 // masked scores; raising the reference lazily changes only fp32 rounding.
 template <int D, typename T>
 E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_t (&q)[D / 32], f32x4_t (&acc)[D / 16],
-                         float& mref, float& lsum, float scale_log2, uint32_t vis, int g) {
+                         float& mref, float& lsum, float scale_log2, uint32_t vis, bool full, int g) {
   constexpr float kSlack = 16.0f;
   // operands are read in groups (K: KG chunks per key row, V: VG d-tiles), a compiler fence after each group: at
   // most two groups are in registers at once (one being multiplied, the next arriving)
@@ -232,10 +232,24 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(kop[kt][c], q[c0 + c], s[kt]);
   }
+  // the V reads' bases for this stage (at D 256 opaque to the compiler, so that 128 (dt / 4) stays the reads'
+  // offset field)
+  uint32_t vb[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      vb[h][v] = off.vb[h][v];
+      if constexpr (D == 256) {
+        vb[h][v] += stage;
+        asm volatile("" : "+v"(vb[h][v]));
+      }
+    }
+  const uint32_t vst = D == 256 ? 0u : stage;
   auto read_v = [&](int dt) {
     const uint32_t o = 128 * (dt >> 2);
-    const v4i16 lo4 = lds_tr16(stage + off.vb[0][dt & 3] + o);
-    const v4i16 hi4 = lds_tr16(stage + off.vb[1][dt & 3] + o);
+    const v4i16 lo4 = lds_tr16(vst + vb[0][dt & 3] + o);
+    const v4i16 hi4 = lds_tr16(vst + vb[1][dt & 3] + o);
     return __builtin_shufflevector(__builtin_bit_cast(u32x2_t, lo4), __builtin_bit_cast(u32x2_t, hi4), 0, 1, 2, 3);
   };
   u32x4_t vop[VG];
@@ -243,16 +257,24 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
   for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);  // the first group lands while the softmax runs
   asm volatile("" ::: "memory");
 
-  const uint32_t vv = vis >> (4 * g);
+  // scaled scores; a tile whose keys are all visible (`full`, wave-uniform) skips the mask
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kt][i] *= scale_log2;
+  if (!full) {
+    asm volatile("");  // a branch, not selects: the common full tile runs none of this
+    const uint32_t vv = vis >> (4 * g);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kt][i] = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] : -INFINITY;
+  }
   float tmax = -INFINITY;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] * scale_log2 : -INFINITY;
-      s[kt][i] = v;
-      tmax = fmaxf(tmax, v);
-    }
+    for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kt][i]);
   if (__any(tmax > mref + kSlack)) {  // rare: a new reference for every row of the wave (max over the row's lanes)
     float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
@@ -296,8 +318,8 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
 // scales of keys 16 kt + 4 g .. + 3.
 template <int D, typename T>
 E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& off, const u32x4_t (&q)[D / 32],
-                             f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis, int g,
-                             const float4 (&ks)[2], const float4 (&vs)[2]) {
+                             f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis,
+                             bool full, int g, const float4 (&ks)[2], const float4 (&vs)[2]) {
   constexpr float kSlack = 16.0f;
   constexpr int KG = 4, VG = 4;
   f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
@@ -317,7 +339,17 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(kraw[kt][c])), q[c0 + c], s[kt]);
   }
-  auto read_v = [&](int dt) { return lds_tr8(vst + off.vb[dt & 7] + 128 * (dt >> 3)); };
+  uint32_t vb[8];  // the V reads' bases (at D 256 opaque, so that 128 (dt / 8) stays the reads' offset field)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    vb[e] = off.vb[e];
+    if constexpr (D == 256) {
+      vb[e] += vst;
+      asm volatile("" : "+v"(vb[e]));
+    }
+  }
+  const uint32_t vsb = D == 256 ? 0u : vst;
+  auto read_v = [&](int dt) { return lds_tr8(vsb + vb[dt & 7] + 128 * (dt >> 3)); };
   uint2 vop[VG];
 #pragma unroll
   for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);
@@ -326,15 +358,22 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
   const uint32_t vv = vis >> (4 * g);
   const float ksc[2][4] = {{ks[0].x, ks[0].y, ks[0].z, ks[0].w}, {ks[1].x, ks[1].y, ks[1].z, ks[1].w}};
   const float vsc[2][4] = {{vs[0].x, vs[0].y, vs[0].z, vs[0].w}, {vs[1].x, vs[1].y, vs[1].z, vs[1].w}};
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kt][i] *= scale_log2 * ksc[kt][i];
+  if (!full) {  // a tile with keys past the context
+    asm volatile("");  // a branch, not selects
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kt][i] = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] : -INFINITY;
+  }
   float tmax = -INFINITY;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] * (scale_log2 * ksc[kt][i]) : -INFINITY;
-      s[kt][i] = v;
-      tmax = fmaxf(tmax, v);
-    }
+    for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kt][i]);
   if (__any(tmax > mref + kSlack)) {
     float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
@@ -752,6 +791,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   if constexpr (FP8) off8 = operand_offsets8<D>(g, l16);
   int piece_j0 = cc.j;
   const int rows_seg = p.rows_seg;
+  // tiles whose keys are all visible skip the mask (at D 256; smaller heads have no registers to spare for it)
+  constexpr bool kFullTiles = D == 256;
 #pragma unroll
   for (int i = 0; i < NS; ++i) __syncthreads();  // the producers' prologue
 
@@ -767,11 +808,12 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
         const float4 ks[2] = {sc[8 * h + g], sc[8 * h + 4 + g]}, vs[2] = {sc[16 + 8 * h + g], sc[16 + 8 * h + 4 + g]};
         consume_tile_fp8<D, T>(lds_addr(smem[slot][0]) + 32 * h * D, lds_addr(smem[slot][1]) + 32 * h * D, off8, q,
                                acc, mref, lsum, scale_log2, visible(false, base + 32 * h, cc.ctx, cc.width, row_mask),
-                               g, ks, vs);
+                               kFullTiles && base + 32 * h + 32 <= cc.ctx, g, ks, vs);
       }
     } else {
       consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
-                         visible(is_new, base, cc.ctx, cc.width, row_mask), g);
+                         visible(is_new, base, cc.ctx, cc.width, row_mask),
+                         kFullTiles && !is_new && base + kTileKeys <= cc.ctx, g);
     }
 
     const bool seg_end = cc.j == cc.tiles - 1;
