@@ -312,34 +312,45 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
   }
 }
 
-// The consumer step for an fp8 context tile: the same schedule, operands widened from fp8 as they are read, and the
-// per-(page, KV head) scales folded in per key — into the scores (s_k q . k8) and into P^T (p s_v, whose sum over keys
-// stays the unscaled softmax denominator) — so the products run on the exact e4m3 values. ks[kt] / vs[kt] hold the
-// scales of keys 16 kt + 4 g .. + 3.
+// The consumer step for an fp8 context tile (64 keys, two 32-key halves at K / V + 32 h D): the same schedule over
+// both halves at once — the four S^T chains (half, kt) in flight together, one softmax step over the 64 scores — with
+// the operands widened from fp8 as they are read and the per-(page, KV head) scales folded in per key: into the
+// scores (s_k q . k8) and into P^T (p s_v, whose sum over keys stays the unscaled softmax denominator), so the
+// products run on the exact e4m3 values. `scl` holds the tile's K scales (keys 0 .. 63) then its V scales.
 template <int D, typename T>
 E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& off, const u32x4_t (&q)[D / 32],
-                             f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis,
-                             bool full, int g, const float4 (&ks)[2], const float4 (&vs)[2]) {
+                             f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2, uint32_t vis0,
+                             uint32_t vis1, bool full, int g, const float4* scl) {
   constexpr float kSlack = 16.0f;
-  constexpr int KG = 4, VG = 4;
-  f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+  constexpr int KG = 2, VG = 4;
+  constexpr uint32_t kHalf = 32 * D;  // bytes from a half's rows to the next half's
+  f32x4_t s[2][2];  // [half][kt]
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) s[h][kt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int c0 = 0; c0 < D / 32; c0 += KG) {
-    uint2 kraw[2][KG];
+    uint2 kraw[2][2][KG];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
-        const int cc = c0 + c;
-        kraw[kt][c] = lds_load8(kst + off.kb[kt][cc & 3] + 128 * (cc >> 2));
-      }
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
+          const int cc = c0 + c;
+          kraw[h][kt][c] = lds_load8(kst + off.kb[kt][cc & 3] + kHalf * h + 128 * (cc >> 2));
+        }
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int c = 0; c < KG && c0 + c < D / 32; ++c)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(kraw[kt][c])), q[c0 + c], s[kt]);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+          s[h][kt] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(kraw[h][kt][c])), q[c0 + c], s[h][kt]);
   }
-  uint32_t vb[8];  // the V reads' bases (at D 256 opaque, so that 128 (dt / 8) stays the reads' offset field)
+  uint32_t vb[8];  // the V reads' bases (at D 256 opaque, so that the half and 128 (dt / 8) stay in the offset field)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     vb[e] = off.vb[e];
@@ -349,31 +360,39 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
     }
   }
   const uint32_t vsb = D == 256 ? 0u : vst;
-  auto read_v = [&](int dt) { return lds_tr8(vsb + vb[dt & 7] + 128 * (dt >> 3)); };
+  auto read_v = [&](int h, int dt) { return lds_tr8(vsb + vb[dt & 7] + kHalf * h + 128 * (dt >> 3)); };
   uint2 vop[VG];
 #pragma unroll
-  for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);
+  for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(0, i);
   asm volatile("" ::: "memory");
 
-  const uint32_t vv = vis >> (4 * g);
-  const float ksc[2][4] = {{ks[0].x, ks[0].y, ks[0].z, ks[0].w}, {ks[1].x, ks[1].y, ks[1].z, ks[1].w}};
-  const float vsc[2][4] = {{vs[0].x, vs[0].y, vs[0].z, vs[0].w}, {vs[1].x, vs[1].y, vs[1].z, vs[1].w}};
+  // scores in the log2 domain: key 32 h + 16 kt + 4 g + i takes its page's K scale
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[kt][i] *= scale_log2 * ksc[kt][i];
+    for (int kt = 0; kt < 2; ++kt) {
+      const float4 k4 = scl[8 * h + 4 * kt + g];
+      const float ksc[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[h][kt][i] *= scale_log2 * ksc[i];
+    }
   if (!full) {  // a tile with keys past the context
     asm volatile("");  // a branch, not selects
+    const uint32_t vv[2] = {vis0 >> (4 * g), vis1 >> (4 * g)};
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s[kt][i] = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] : -INFINITY;
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[h][kt][i] = ((vv[h] >> (16 * kt + i)) & 1u) ? s[h][kt][i] : -INFINITY;
   }
   float tmax = -INFINITY;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kt][i]);
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[h][kt][i]);
   if (__any(tmax > mref + kSlack)) {
     float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
@@ -385,31 +404,38 @@ E4_DEV void consume_tile_fp8(uint32_t kst, uint32_t vst, const OperandOffsets8& 
     for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
   }
   const float ref = mref == -INFINITY ? 0.f : mref;
-  uint32_t w[4];
+  u32x4_t pb[2];
 #pragma unroll
-  for (int p = 0; p < 4; ++p) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4
-    const int kt = p >> 1, i0 = 2 * (p & 1);
-    const float p0 = __builtin_amdgcn_exp2f(s[kt][i0] - ref);
-    const float p1 = __builtin_amdgcn_exp2f(s[kt][i0 + 1] - ref);
-    lsum += p0 + p1;
-    w[p] = pack2<T>(p0 * vsc[kt][i0], p1 * vsc[kt][i0 + 1]);
-  }
-  const u32x4_t pb = {w[0], w[1], w[2], w[3]};
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-  for (int d0 = 0; d0 < D / 16; d0 += VG) {
-    uint2 nxt[VG];
-    if (d0 + VG < D / 16) {
-#pragma unroll
-      for (int i = 0; i < VG; ++i) nxt[i] = read_v(d0 + VG + i);
+    for (int kt = 0; kt < 2; ++kt) {  // element i of P^T's operand is key 16 (i / 4) + 4 g + i % 4 of the half
+      const float4 v4 = scl[16 + 8 * h + 4 * kt + g];
+      const float p0 = __builtin_amdgcn_exp2f(s[h][kt][0] - ref), p1 = __builtin_amdgcn_exp2f(s[h][kt][1] - ref);
+      const float p2 = __builtin_amdgcn_exp2f(s[h][kt][2] - ref), p3 = __builtin_amdgcn_exp2f(s[h][kt][3] - ref);
+      lsum += (p0 + p1) + (p2 + p3);
+      pb[h][2 * kt] = pack2<T>(p0 * v4.x, p1 * v4.y);
+      pb[h][2 * kt + 1] = pack2<T>(p2 * v4.z, p3 * v4.w);
     }
-    asm volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(vop[i])), pb, acc[d0 + i]);
-    if (d0 + VG < D / 16) {
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < VG; ++i) vop[i] = nxt[i];
+    for (int d0 = 0; d0 < D / 16; d0 += VG) {
+      // the next group's V reads: this half's next d-tiles, or the second half's first
+      const bool last = d0 + VG >= D / 16;
+      uint2 nxt[VG];
+      if (!(last && h == 1)) {
+#pragma unroll
+        for (int i = 0; i < VG && i < D / 16; ++i) nxt[i] = last ? read_v(1, i) : read_v(h, d0 + VG + i);
+      }
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < VG && d0 + i < D / 16; ++i)
+        acc[d0 + i] = mfma16<T>(__builtin_bit_cast(u32x4_t, widen_fp8x8<T>(vop[i])), pb[h], acc[d0 + i]);
+      if (!(last && h == 1)) {
+#pragma unroll
+        for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = nxt[i];
+      }
     }
-  }
 }
 
 // Visible keys of a tile for one row: context tiles, positions below the context length; draft tiles, draft rows
@@ -801,15 +827,12 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     __syncthreads();
     const bool is_new = cc.j >= cc.n_ctx;
     const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * CK;
-    if (FP8 && !is_new) {  // two 32-key halves of the 64-key fp8 tile
-      const float4* sc = reinterpret_cast<const float4*>(s_scl[FP8 ? slot : 0]);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float4 ks[2] = {sc[8 * h + g], sc[8 * h + 4 + g]}, vs[2] = {sc[16 + 8 * h + g], sc[16 + 8 * h + 4 + g]};
-        consume_tile_fp8<D, T>(lds_addr(smem[slot][0]) + 32 * h * D, lds_addr(smem[slot][1]) + 32 * h * D, off8, q,
-                               acc, mref, lsum, scale_log2, visible(false, base + 32 * h, cc.ctx, cc.width, row_mask),
-                               kFullTiles && base + 32 * h + 32 <= cc.ctx, g, ks, vs);
-      }
+    if (FP8 && !is_new) {  // the 64-key fp8 tile
+      consume_tile_fp8<D, T>(lds_addr(smem[slot][0]), lds_addr(smem[slot][1]), off8, q, acc, mref, lsum, scale_log2,
+                             visible(false, base, cc.ctx, cc.width, row_mask),
+                             visible(false, base + 32, cc.ctx, cc.width, row_mask),
+                             kFullTiles && base + kTileKeys8 <= cc.ctx, g,
+                             reinterpret_cast<const float4*>(s_scl[FP8 ? slot : 0]));
     } else {
       consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
                          visible(is_new, base, cc.ctx, cc.width, row_mask),
