@@ -98,9 +98,14 @@ struct Tile8 {
 };
 
 // A 32-key tile of K and of V lives in LDS row-major (rows of D 16-bit values) with its 16-byte chunks XOR-swizzled
-// per row, so both MFMA operand reads are conflict-free: K chunk c of key k sits at c ^ (k & 7); V chunk c at
-// c ^ 2 (k & 3). Direct loads (global_load_lds: lane p of an instruction fills 16-byte slot p of a 1 KB run) fetch
-// for each slot the chunk the swizzle puts there.
+// per row, so both MFMA operand reads are conflict-free on gfx950's LDS, which serves 256 bytes a cycle: 16 lanes of a
+// 16-byte read (K: 16 consecutive key rows at one d offset) and 32 lanes of the transposing 8-byte read (V: 8 key rows,
+// 32 bytes each) must fall in distinct 16- / 8-byte slots of a 256-byte window. With R = rows per 256 bytes (1 at
+// D >= 128), K chunk c of key k sits at c ^ ((k / R) & (16 / R - 1)) and V chunk c at c ^ 2 ((k / R) & (8 / R - 1)).
+// (Measured on the device, 4 waves per CU reading concurrently: a 3-bit K swizzle at D 256 took 34 cycles per read
+// against 21 for this one and for linear addresses; the 2-bit V swizzle 20.5 against 18.) Direct loads
+// (global_load_lds: lane p of an instruction fills 16-byte slot p of a 1 KB run) fetch for each slot the chunk the
+// swizzle puts there.
 template <int D>
 struct Tile {
   static constexpr int CH = D / 8;           // 16-byte chunks per row
@@ -108,8 +113,11 @@ struct Tile {
   static constexpr int BYTES = kTileKeys * ROWB;
   static constexpr int RPI = 1024 / ROWB;    // rows one direct-load instruction fills (64 lanes x 16 bytes)
   static constexpr int NI = kTileKeys / RPI;  // instructions per matrix per tile
-  static E4_DEV int kswz(int row) { return row & (CH < 8 ? CH - 1 : 7); }
-  static E4_DEV int vswz(int row) { return (2 * (row & 3)) & (CH - 1); }
+  static constexpr int R = ROWB >= 256 ? 1 : 256 / ROWB;  // rows per 256-byte window
+  static constexpr int KB = 4 / R;  // K chunk groups 4 c + g whose index bits the swizzle reaches (c % KB)
+  static constexpr int VB = 8 / R;  // V d-tiles (chunk pairs 2 dt, 2 dt + 1) whose index bits it reaches (dt % VB)
+  static constexpr E4_DEV int kswz(int row) { return (row / R) & (16 / R - 1); }
+  static constexpr E4_DEV int vswz(int row) { return 2 * ((row / R) & (8 / R - 1)); }
 };
 
 // One tile for a wave's 16 query rows (lane l16 of each 16-lane group owns row l16; g = lane / 16):
@@ -230,6 +238,7 @@ constexpr int kStreamMaxReqs = 1024;  // per-request query starts and contexts a
 
 struct StreamPlan {
   int G, row_tiles, C, RG, HR, rows_seg, nwg, direct, fp8;
+  int seg_cost;  // a segment's end in quarter tiles, for the cost-weighted shares
   int64_t part_off, lse_off;  // float offsets into the workspace (the int64 prefix of tiles per request is first)
 };
 

@@ -31,6 +31,7 @@ namespace e4attn {
 constexpr int kStages = 4;            // power of two
 constexpr int kProducers = 2;
 constexpr int kMinTilesPerGroup = 8;  // small jobs use fewer, longer shares
+constexpr int kAheadTiles = 4;        // tiles before a segment's end that its successor's rows are loaded (16-bit pages)
 
 namespace {
 
@@ -129,33 +130,27 @@ E4_DEV v4i16 lds_tr16(uint32_t addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)static_cast<uintptr_t>(addr));
 }
 
-// Per-lane LDS offsets of a consumer's operand reads within a stage. The swizzles XOR only the low three bits of a
-// 16-byte chunk index, so each read is a base plus an immediate: K chunk 4 c + g of key row 16 kt + l16 sits at
-// kb[kt][c & 1] + 128 (c >> 1); the transposing V reads of d-tile dt (keys 4 g + j and 16 + 4 g + j, j = l16 / 4)
-// at vb[h][dt & 3] + 128 (dt >> 2).
+// Per-lane LDS offsets of a consumer's operand reads within a stage. The swizzles XOR only the chunk-index bits that
+// Tile::KB / Tile::VB count, and rows 16 apart share a swizzle, so each read is a base plus an immediate: K chunk
+// 4 c + g of key row 16 kt + l16 sits at kb[c % KB] + 16 ROWB kt + 64 KB (c / KB); the transposing V reads of d-tile dt
+// (keys 16 h + 4 g + j, h = 0, 1, j = l16 / 4) at vb[dt % VB] + 16 ROWB h + 32 VB (dt / VB).
 struct OperandOffsets {
-  uint32_t kb[2][2];
-  uint32_t vb[2][4];
+  uint32_t kb[4];
+  uint32_t vb[8];
 };
 
 template <int D>
 E4_DEV OperandOffsets operand_offsets(int g, int l16) {
   using TL = Tile<D>;
-  OperandOffsets o;
+  static_assert(TL::kswz(16) == TL::kswz(0) && TL::vswz(16) == TL::vswz(0), "rows 16 apart share a swizzle");
+  OperandOffsets o = {};
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int key = 16 * kt + l16;
-#pragma unroll
-    for (int e = 0; e < 2; ++e) o.kb[kt][e] = key * TL::ROWB + 16 * ((4 * e + g) ^ TL::kswz(key));
-  }
+  for (int e = 0; e < TL::KB; ++e) o.kb[e] = l16 * TL::ROWB + 16 * ((4 * e + g) ^ TL::kswz(l16));
   const int j = l16 >> 2, s4 = l16 & 3;
+  const int key = 4 * g + j;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int key = 16 * h + 4 * g + j;
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-      o.vb[h][v] = TL::BYTES + key * TL::ROWB + 16 * ((2 * v + (s4 >> 1)) ^ TL::vswz(key)) + 8 * (s4 & 1);
-  }
+  for (int v = 0; v < TL::VB; ++v)
+    o.vb[v] = TL::BYTES + key * TL::ROWB + 16 * ((2 * v + (s4 >> 1)) ^ TL::vswz(key)) + 8 * (s4 & 1);
   return o;
 }
 
@@ -214,7 +209,11 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
   // operands are read in groups (K: KG chunks per key row, V: VG d-tiles), a compiler fence after each group: at
   // most two groups are in registers at once (one being multiplied, the next arriving)
   constexpr int KG = 4, VG = 4;
-  const uint32_t kb[2][2] = {{stage + off.kb[0][0], stage + off.kb[0][1]}, {stage + off.kb[1][0], stage + off.kb[1][1]}};
+  using TL = Tile<D>;
+  constexpr int KB = TL::KB, VB = TL::VB;
+  uint32_t kb[KB];
+#pragma unroll
+  for (int e = 0; e < KB; ++e) kb[e] = stage + off.kb[e];
   f32x4_t s[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int c0 = 0; c0 < D / 32; c0 += KG) {
@@ -224,7 +223,7 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
 #pragma unroll
       for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
         const int cc = c0 + c;
-        kop[kt][c] = lds_load16(kb[kt][cc & 1] + 128 * (cc >> 1));
+        kop[kt][c] = lds_load16(kb[cc % KB] + 16 * TL::ROWB * kt + 64 * KB * (cc / KB));
       }
     asm volatile("" ::: "memory");
 #pragma unroll
@@ -232,24 +231,22 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(kop[kt][c], q[c0 + c], s[kt]);
   }
-  // the V reads' bases for this stage (at D 256 opaque to the compiler, so that 128 (dt / 4) stays the reads'
+  // the V reads' bases for this stage (at D 256 opaque to the compiler, so that 32 VB (dt / VB) stays the reads'
   // offset field)
-  uint32_t vb[2][4];
+  uint32_t vb[VB];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      vb[h][v] = off.vb[h][v];
-      if constexpr (D == 256) {
-        vb[h][v] += stage;
-        asm volatile("" : "+v"(vb[h][v]));
-      }
+  for (int v = 0; v < VB; ++v) {
+    vb[v] = off.vb[v];
+    if constexpr (D == 256) {
+      vb[v] += stage;
+      asm volatile("" : "+v"(vb[v]));
     }
+  }
   const uint32_t vst = D == 256 ? 0u : stage;
   auto read_v = [&](int dt) {
-    const uint32_t o = 128 * (dt >> 2);
-    const v4i16 lo4 = lds_tr16(vst + vb[0][dt & 3] + o);
-    const v4i16 hi4 = lds_tr16(vst + vb[1][dt & 3] + o);
+    const uint32_t o = 32 * VB * (dt / VB);
+    const v4i16 lo4 = lds_tr16(vst + vb[dt % VB] + o);
+    const v4i16 hi4 = lds_tr16(vst + vb[dt % VB] + 16 * TL::ROWB + o);
     return __builtin_shufflevector(__builtin_bit_cast(u32x2_t, lo4), __builtin_bit_cast(u32x2_t, hi4), 0, 1, 2, 3);
   };
   u32x4_t vop[VG];
@@ -486,6 +483,32 @@ E4_DEV void wait_vm_dyn(int n) {
 }
 #undef E4_WAIT_CASE
 
+// The rows of a finished piece, with the same stores on every path (no branch): normalised rows of dtype T to `out`
+// (ooff: the lane's row from obase, in bytes) when the segment ends here, else fp32 partials normalised by their own
+// sum and their log2-sum-exp to the workspace (poff / loff: the lane's partial row and lse word). A store that does not
+// apply — the other kind, a lane without a row, the lse from lanes g != 0 — is addressed past its buffer's range
+// (offset kDropped, or a range of zero bytes) and dropped. A fixed store count after the next segment's query loads lets
+// the compiler wait for exactly those loads, where a branch on the kind made it wait for every store (vmcnt(0)).
+constexpr uint32_t kDropped = 0x7ffffff0u;
+
+template <int D, typename T>
+E4_DEV void store_piece(const f32x4_t (&acc)[D / 16], float ls, float mref, bool fin, uint16_t* obase, uint32_t ooff,
+                        float* pbase, uint32_t poff, float* lbase, uint32_t loff, int g) {
+  const float inv = ls > 0.f ? 1.0f / ls : 0.f;
+  const float lse = ls > 0.f ? mref + log2f(ls) : -INFINITY;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(obase, 0, fin ? kDropped : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(pbase, 0, fin ? 0 : kDropped, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(lbase, 0, fin ? 0 : kDropped, 0x00020000);
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    const f32x4_t v = acc[dt] * inv;
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])}, ro,
+                                          ooff + 2 * (16 * dt + 4 * g), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, poff + 4 * (16 * dt + 4 * g), 0, 0);
+  }
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl, loff, 0, 0);
+}
+
 constexpr int waves_per_eu(int d) { return d == 256 ? 2 : (d == 128 ? 3 : 4); }
 
 // One workgroup: C consumer waves (16 query rows each) and kProducers producer waves (page lookups, direct loads).
@@ -507,10 +530,17 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   __shared__ int s_ctx[kStreamMaxReqs];
   __shared__ int64_t s_wsum[NW];
   __shared__ int64_t s_start[2];
+  __shared__ int64_t s_share[2];  // this share's first tile and the next share's
   __shared__ __attribute__((aligned(16))) float s_scl[FP8 ? NS : 1][2 * kTileKeys8];  // fp8: K, V scales per key
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = uni(tid >> 6);
+  // Roles. Waves go to the CU's four SIMDs round-robin (wave w on SIMD w % 4). With six consumers on 16-bit pages the
+  // producers take waves 0 and 4, a SIMD of their own, so their issue never queues behind consumer MFMA and VALU
+  // work (per-tile interval 1.57 -> 1.45 us at batch 64); fp8 consumers are VALU-bound and keep all four SIMDs.
+  constexpr bool kOwnSimd = C == 6 && !FP8;
+  const bool producer = kOwnSimd ? (wave & 3) == 0 : wave >= C;
+  const int cw = kOwnSimd ? (wave >> 2) * 3 + (wave & 3) - 1 : wave;  // consumer index (producers: unused)
   const int g = lane >> 4, l16 = lane & 15;
   const int B = a.num_reqs;
   const int HR = p.HR;
@@ -525,11 +555,19 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     }
   }
   __syncthreads();
+  // Shares split the sequence by cost, not by tiles: a tile costs 4 units and a segment's end (its rows stored, the
+  // next segment's loaded) p.seg_cost more, so that shares holding more segment ends hold fewer tiles. Each thread
+  // takes a range of requests; (tiles | non-empty requests << 40) is scanned over the workgroup.
+  constexpr int kCnt = 40;
+  constexpr int64_t kTileMask = (int64_t(1) << kCnt) - 1;
   const int per = (B + NT - 1) / NT;
   const int b_lo = tid * per < B ? tid * per : B;
   const int b_hi = b_lo + per < B ? b_lo + per : B;
   int64_t mine = 0;
-  for (int b = b_lo; b < b_hi; ++b) mine += tiles_of<CK>(s_qsl, s_ctx, b);
+  for (int b = b_lo; b < b_hi; ++b) {
+    const int tb = tiles_of<CK>(s_qsl, s_ctx, b);
+    mine += tb + (tb > 0 ? int64_t(1) << kCnt : 0);
+  }
   int64_t incl = mine;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -545,24 +583,48 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     before += w2 < wave ? v : 0;
     total += v;
   }
-  const int64_t tiles_all = total * HR;
+  const int64_t total_t = total & kTileMask;
+  const int64_t tiles_all = total_t * HR;
   const int64_t nact = active_groups(tiles_all, p.nwg);
+  const int64_t E = p.seg_cost;
+  const int64_t cost_all = HR * (4 * total_t + E * (total >> kCnt));
   const int w = blockIdx.x;
-  const int64_t g0 = nact > 0 ? tiles_all * w / nact : 0;
-  const int64_t g1 = nact > 0 ? tiles_all * (w + 1) / nact : 0;
+  const int64_t c0 = nact > 0 ? cost_all * w / nact : 0, c1 = nact > 0 ? cost_all * (w + 1) / nact : 0;
+  int64_t* const pre = reinterpret_cast<int64_t*>(a.workspace);  // [B + 1] tiles before each request, then shares
   {
-    int64_t* pre = reinterpret_cast<int64_t*>(a.workspace);
-    int64_t run = before;
+    int64_t run_t = before & kTileMask, run_n = before >> kCnt;
     for (int b = b_lo; b < b_hi; ++b) {
       const int tb = tiles_of<CK>(s_qsl, s_ctx, b);
-      if (w == 0) pre[b] = run;
+      if (w == 0) pre[b] = run_t;
+      if (tb > 0) {
+        const int64_t cb = HR * (4 * run_t + E * run_n), sc = 4 * tb + E;  // cost before b; of one of its segments
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int64_t c = i == 0 ? c0 : c1;
+          if (cb <= c && c < cb + HR * sc) {  // the first tile at or past cost c; past a segment's last tile: the next
+            const int64_t k = (c - cb) / sc, u = c - cb - k * sc;
+            s_share[i] = run_t * HR + (u > 4 * (tb - 1) ? (k + 1) * tb : k * tb + (u + 3) / 4);
+          }
+        }
+        run_t += tb;
+        run_n += 1;
+      }
+    }
+    if (w == 0 && tid == 0) pre[B] = total_t;
+  }
+  __syncthreads();
+  const int64_t g0 = c0 < cost_all ? s_share[0] : tiles_all;
+  const int64_t g1 = c1 < cost_all ? s_share[1] : tiles_all;
+  {
+    int64_t run = before & kTileMask;
+    for (int b = b_lo; b < b_hi; ++b) {
+      const int tb = tiles_of<CK>(s_qsl, s_ctx, b);
       if (tb > 0 && run * HR <= g0 && g0 < (run + tb) * HR) {
         s_start[0] = b;
         s_start[1] = run;
       }
       run += tb;
     }
-    if (w == 0 && tid == 0) pre[B] = total;
   }
   __syncthreads();
   if (w >= nact || g0 >= g1) return;
@@ -578,8 +640,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   }
   const int RG = p.RG;
 
-  if (wave >= C) {  // ---- producers ---------------------------------------------------------------------------------
-    const int pi = wave - C;  // producer 0 also runs the page lookups
+  if (producer) {  // ---- producers ---------------------------------------------------------------------------------
+    const int pi = kOwnSimd ? wave >> 2 : wave - C;  // producer 0 also runs the page lookups
     Cursor cd = cc, cl = cc;
     const int page = a.page;
     const int page_shift = (page & (page - 1)) == 0 ? __builtin_ctz(page) : -1;
@@ -794,7 +856,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   auto enter = [&](const Cursor& c, u32x4_t (&qr)[D / 32], int64_t& mask_r, bool& ok_r, int& t_r, int& head_r) {
     const int kvh = c.k / RG, rg = c.k - kvh * RG;
     const int rows = c.width < a.max_query_len ? c.width : a.max_query_len;
-    const int rt = rg * C + wave;
+    const int rt = rg * C + cw;
     const int rho = rt * 16 + l16;
     t_r = rho / G;
     head_r = kvh * G + (rho - t_r * G);
@@ -817,14 +879,36 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   if constexpr (FP8) off8 = operand_offsets8<D>(g, l16);
   int piece_j0 = cc.j;
   const int rows_seg = p.rows_seg;
+  // 16-bit pages: the next segment's rows are loaded kAheadTiles tiles before this segment ends, into qn / mask_n.
+  // Loaded at the end, they waited behind the K / V stream this CU has in flight (~2 us per segment end).
+  constexpr bool kPrefetch = !FP8;
+  u32x4_t qn[kPrefetch ? D / 32 : 1];
+  int64_t mask_n = 0;
+  bool ok_n = false, fetched = false;
+  int t_n = 0, head_n = 0;
+  Cursor cn = cc;
   // tiles whose keys are all visible skip the mask (at D 256; smaller heads have no registers to spare for it)
   constexpr bool kFullTiles = D == 256;
+  // the first rows' loads waited for here, so that the loop's wait for a segment's rows (loaded before the previous
+  // piece's stores) is not merged with a wait made for these
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) asm volatile("" ::"v"(q[i]));
+  asm volatile("" ::"v"(row_mask));
 #pragma unroll
   for (int i = 0; i < NS; ++i) __syncthreads();  // the producers' prologue
 
   for (int64_t x = g0; x < g1; ++x) {
     const int slot = static_cast<int>(x & (NS - 1));
     __syncthreads();
+    if constexpr (kPrefetch) {
+      if (!fetched && cc.tiles - 1 - cc.j <= kAheadTiles && x + (cc.tiles - cc.j) < g1) {  // the next segment is ours
+        cn = cc;
+        cn.j = cn.tiles - 1;
+        cur_next<CK>(cn, s_qsl, s_ctx, B, HR);
+        enter(cn, qn, mask_n, ok_n, t_n, head_n);
+        fetched = true;
+      }
+    }
     const bool is_new = cc.j >= cc.n_ctx;
     const int base = is_new ? (cc.j - cc.n_ctx) * kTileKeys : cc.j * CK;
     if (FP8 && !is_new) {  // the 64-key fp8 tile
@@ -840,37 +924,48 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     }
 
     const bool seg_end = cc.j == cc.tiles - 1;
+    if ((cc.j == 0 || seg_end) && cw == 0) {  // the shares holding the segment's first and last tiles (every lane
+                                               // stores the same word: no lane branch inside the loop)
+      int32_t* const seg_w = reinterpret_cast<int32_t*>(pre + B + 1) + 2 * (static_cast<int64_t>(cc.b) * HR + cc.k);
+      if (cc.j == 0) seg_w[0] = w;
+      if (seg_end) seg_w[1] = w;
+    }
     if (seg_end || x == g1 - 1) {
-      // the next segment's rows first (16-bit pages at D 256; elsewhere the registers are not there): their q / mask
-      // loads go out before this segment's stores, so the wait for them (vmcnt retires in issue order) is not a wait
-      // for the stores
-      constexpr bool kAhead = !FP8 && D == 256;
       const bool more = x + 1 < g1;
-      Cursor cn = cc;
-      u32x4_t qn[D / 32];
-      int64_t mask_n = 0;
-      bool ok_n = false;
-      int t_n = 0, head_n = 0;
-      if (kAhead && more) {
-        cur_next<CK>(cn, s_qsl, s_ctx, B, HR);
-        enter(cn, qn, mask_n, ok_n, t_n, head_n);
-      }
       float ls = lsum + __shfl_xor(lsum, 16, 64);
       ls += __shfl_xor(ls, 32, 64);
-      if (row_ok) {
+      // where this piece's rows go: a segment finished here to `out`; a piece of a cut segment to slot 2 w (the share's
+      // first piece, it starts inside a segment) or 2 w + 1 (its last, it ends inside one)
+      const bool fin = piece_j0 == 0 && seg_end;
+      uint16_t* const obase = static_cast<uint16_t*>(a.out) + cc.qs * a.stride_ot;
+      const uint32_t ooff = row_ok ? static_cast<uint32_t>((t * a.stride_ot + head * a.stride_oh) * 2) : kDropped;
+      const int64_t part = (piece_j0 > 0 ? 2 * w : 2 * w + 1) * static_cast<int64_t>(rows_seg) + 16 * cw + l16;
+      const uint32_t poff = row_ok ? static_cast<uint32_t>(part * D * 4) : kDropped;
+      const uint32_t loff = row_ok && g == 0 ? static_cast<uint32_t>(part * 4) : kDropped;
+      // The next segment's rows: 16-bit pages prefetched them into qn (at the latest on this tile, so always when there
+      // is a next segment); fp8 pages below D 128 load them here, straight into q and row_mask before this piece's
+      // stores; fp8 pages at D >= 128 have no registers for q and the accumulators at once and load them after. A load
+      // before the stores is waited for with the stores' count (vmcnt retires in issue order), not behind them; the
+      // branch-free stores keep that count the same on every path.
+      constexpr bool kAhead = !FP8 || D < 128;
+      if (!kPrefetch && kAhead && more) {
+        cur_next<CK>(cc, s_qsl, s_ctx, B, HR);
+        enter(cc, q, row_mask, row_ok, t, head);
+      }
+      if constexpr (kAhead) {
+        store_piece<D, T>(acc, ls, mref, fin, obase, ooff, a.workspace + p.part_off, poff, a.workspace + p.lse_off,
+                          loff, g);
+      } else if (row_ok) {  // registers too short for the branch-free form; these waves wait for their stores anyway
         const float inv = ls > 0.f ? 1.0f / ls : 0.f;
-        if (piece_j0 == 0 && seg_end) {
-          store_rows<D, T>(static_cast<uint16_t*>(a.out) + (cc.qs + t) * a.stride_ot + head * a.stride_oh, acc, inv,
-                           g);
+        if (fin) {
+          store_rows<D, T>(obase + t * a.stride_ot + head * a.stride_oh, acc, inv, g);
         } else {
-          // slot 2 w: the share's first piece (it starts inside a segment); 2 w + 1: its last (it ends inside one)
-          const int64_t part = (piece_j0 > 0 ? 2 * w : 2 * w + 1) * static_cast<int64_t>(rows_seg) + 16 * wave + l16;
           store_partial<D>(a.workspace + p.part_off + part * D, acc, inv, g);
           if (g == 0) a.workspace[p.lse_off + part] = ls > 0.f ? mref + log2f(ls) : -INFINITY;
         }
       }
       if (more) {
-        if constexpr (kAhead) {
+        if constexpr (kPrefetch) {
           cc = cn;
 #pragma unroll
           for (int i = 0; i < D / 32; ++i) q[i] = qn[i];
@@ -878,7 +973,8 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
           row_ok = ok_n;
           t = t_n;
           head = head_n;
-        } else {
+          fetched = false;
+        } else if constexpr (!kAhead) {
           cur_next<CK>(cc, s_qsl, s_ctx, B, HR);
           enter(cc, q, row_mask, row_ok, t, head);
         }
@@ -905,11 +1001,9 @@ __global__ __launch_bounds__(256) void verify_stream_merge(const eagle4_attn_arg
   const int64_t* pre = reinterpret_cast<const int64_t*>(a.workspace);
   const int64_t tiles = pre[b + 1] - pre[b];
   if (tiles <= 0) return;
-  const int64_t tiles_all = pre[a.num_reqs] * p.HR;
-  const int64_t nact = active_groups(tiles_all, p.nwg);
-  const int64_t start = pre[b] * p.HR + k * tiles, end = start + tiles;
-  // the shares holding the segment's first and last tiles (share w covers [floor(T w / n), floor(T (w + 1) / n)))
-  const int64_t w0 = ((start + 1) * nact - 1) / tiles_all, w1 = (end * nact - 1) / tiles_all;
+  // the shares that computed the segment's first and last tiles (recorded by the stream kernel in this launch)
+  const int32_t* const seg_w = reinterpret_cast<const int32_t*>(pre + a.num_reqs + 1) + 2 * static_cast<int64_t>(s);
+  const int64_t w0 = seg_w[0], w1 = seg_w[1];
   if (w0 == w1) return;  // inside one share: written directly
   const int item = blockIdx.y * 256 + threadIdx.x;
   const int rows_seg = p.rows_seg;
@@ -1039,7 +1133,12 @@ int with_config(const eagle4_attn_args& a, int c, F&& go) {
 // by the caller.
 bool stream_covered(const eagle4_attn_args& a) {
   const bool fp8 = a.cache_dtype == EAGLE4_FP8_E4M3 && a.k_scale != nullptr && a.v_scale != nullptr;
-  return (a.cache_dtype == a.dtype || fp8) && a.num_reqs <= kStreamMaxReqs && a.chunk <= 0 && !small_attention_job(a);
+  // a request's output rows are addressed by 32-bit byte offsets from its first row (the branch-free stores)
+  const int64_t span = (static_cast<int64_t>(a.max_query_len) * a.stride_ot + static_cast<int64_t>(a.Hq) * a.stride_oh +
+                        a.D) * 2;
+  const bool rows_ok = a.stride_ot >= 0 && a.stride_oh >= 0 && span < (int64_t(1) << 30);
+  return (a.cache_dtype == a.dtype || fp8) && rows_ok && a.num_reqs <= kStreamMaxReqs && a.chunk <= 0 &&
+         !small_attention_job(a);
 }
 
 bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
@@ -1068,9 +1167,20 @@ bool stream_plan(const eagle4_attn_args& a, StreamPlan& p) {
   if (p.nwg <= 0) return false;
   const int64_t slots = 2 * static_cast<int64_t>(p.nwg);  // a share's first and last piece
   const int64_t rows_seg = p.rows_seg;
-  p.part_off = (2 * (static_cast<int64_t>(a.num_reqs) + 1) + 63) / 64 * 64;
+  // a segment's end, in quarter tiles: its rows' query loads and output stores (96 rows at D 256: 4.5 tiles' time,
+  // measured at batch 64), the stores counted at 1.5 times their bytes; kept below seven tiles, so that no share's
+  // cost span (at least 8 tiles) can fall between two tiles
+  {
+    const int64_t tile_bytes = static_cast<int64_t>(kTileKeys) * a.D * 2 * 2;
+    const int64_t end_bytes = static_cast<int64_t>(p.rows_seg) * a.D * 2 * 2;
+    const int64_t e = (4 * 3 * end_bytes + tile_bytes) / (2 * tile_bytes);
+    p.seg_cost = p.fp8 ? 0 : static_cast<int>(e < 24 ? e : 24);  // fp8 tiles are compute-bound: not measured
+  }
+  // workspace: tiles before each request (int64 [B + 1]), the shares holding each segment's first and last tiles
+  // (int32 [B HR][2]), partials, lse
+  p.part_off = (2 * (static_cast<int64_t>(a.num_reqs) + 1) + 2 * static_cast<int64_t>(a.num_reqs) * p.HR + 63) / 64 * 64;
   p.lse_off = p.part_off + slots * rows_seg * a.D;
-  return true;
+  return slots * rows_seg * a.D * 4 < (int64_t(1) << 30);  // partial rows addressed by 32-bit byte offsets
 }
 
 int64_t stream_workspace_bytes(const StreamPlan& p, const eagle4_attn_args&) {
