@@ -78,6 +78,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __shared__ __align__(16) float s_k[TS][K];
   __shared__ IS s_v[TS][ROWS];
   __shared__ float4 s_sc[TS];  // decay, beta, scale / |q|, 1 / |k|
+  __shared__ float s_out[TS][ROWS];  // the staged nodes' outputs, stored in one pass after the walk
   auto& s_qr = *reinterpret_cast<IS(*)[TS][K]>(s_stack);
   auto& s_kr = *reinterpret_cast<IS(*)[TS][K]>(s_stack + TS * K * sizeof(IS));
   // The walk plan's scratch while wave 0 builds it and hands it over: in s_q, which is first written after the
@@ -184,6 +185,9 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __syncthreads();  // the raw rows' space becomes the stack
 
   settle_loads();  // the initial state and the plan tables
+  // lane u: the element offset of row u's snapshot slot (-1: a pad slot, never written), so that a node's store
+  // address is one readlane and an add
+  const int64_t my_off = my_slot > a.pad_slot_id ? my_slot * a.stride_snap_slot + lane * a.stride_snap_row : -1;
   // A node's inputs: staged nodes from LDS, later ones (T > TS) from global memory with their scalars computed here.
   auto fetch = [&](NodeIn<E, RPT, IS>& nd, int u) {
     if (u < TS) {
@@ -292,22 +296,27 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
       o[s] = e4::group_sum<C>(hq);
     }
     const int64_t t = bos + u;
-    if (c == 0) {
+    if (u < TS) {  // every lane of a row holds its sum: all write it (no lane branch in the walk)
+#pragma unroll
+      for (int s = 0; s < RPT; ++s) s_out[u][lrow[s]] = o[s];
+    } else if (c == 0) {
 #pragma unroll
       for (int s = 0; s < RPT; ++s)
         if (rows[s] < a.V) e4::store_scalar(a.out, t * a.stride_o + static_cast<int64_t>(hv) * a.V + rows[s], a.out_dtype, o[s]);
     }
-    int64_t slot = cache_idx;
-    if (a.row_slots) {
-      if (dfs) {
-        slot = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), u));
-      } else {
+    int64_t off = -1;  // the node's snapshot, elements from snap before head_off
+    if (a.row_slots && dfs) {
+      off = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_off), u));
+    } else {
+      int64_t slot = cache_idx;
+      if (a.row_slots) {
         slot = uni64(e4::ld(a.snap_indices, n, u));
         settle_loads();
       }
+      if (slot > a.pad_slot_id) off = slot * a.stride_snap_slot + static_cast<int64_t>(u) * a.stride_snap_row;
     }
-    if (slot > a.pad_slot_id) {
-      SS* dst = snap_at(slot, u);
+    if (off >= 0) {
+      SS* dst = snap + off + head_off;
       if (full_tile && snap_nt) {
         const __amdgpu_buffer_rsrc_t r = e4walk::buffer_rsrc(dst, a.V * K * static_cast<int>(sizeof(SS)));
 #pragma unroll
@@ -392,6 +401,12 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
         fetch(cur, next);
     }
     u = next;
+  }
+  // the staged nodes' outputs: each wave its own rows (written above by this wave; in-order LDS), node-major
+  for (int i = lane; i < ts * ROWS_WAVE; i += 64) {
+    const int t = i / ROWS_WAVE, lr = wave * ROWS_WAVE + i % ROWS_WAVE, row = row0 + lr;
+    if (row < a.V)
+      e4::store_scalar(a.out, (bos + t) * a.stride_o + static_cast<int64_t>(hv) * a.V + row, a.out_dtype, s_out[t][lr]);
   }
 }
 
