@@ -162,7 +162,25 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
       hist[j * kChannels + c] = c < nch ? state[c * a.stride_cs_dim + (history + j) * a.stride_cs_tok] : 0;
     }
   }
-  if (xvec || row_roll) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the direct loads have landed
+  // this thread's octet of the bias, as raw bits, loaded with the staging so that the wait below covers it (a load
+  // left in flight here would make the compiler wait for every store before the roll)
+  uint32_t bias_raw[8];
+  {
+    const int c0 = 8 * (tid % kVecs);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bias_raw[e] = 0u;
+      if (a.bias != nullptr && c0 + e < nch) {
+        const int64_t i = cb + c0 + e;
+        bias_raw[e] = a.bias_dtype == EAGLE4_F32 ? static_cast<const uint32_t*>(a.bias)[i]
+                                                 : static_cast<const uint16_t*>(a.bias)[i];
+      }
+    }
+  }
+  // the direct loads have landed: vmcnt(0) as the builtin, which the compiler's own wait placement sees (after an
+  // opaque asm wait it would wait again before the first LDS read behind every direct load, and that wait would
+  // also cover the output stores issued by then: the roll behind all of them)
+  if (xvec || row_roll) __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
   // ---- outputs: thread (token lane tl, vector v) computes channels 8 v .. 8 v + 7 of nodes tl, tl + kTokLanes, ... ---
@@ -178,7 +196,9 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
     float bias[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      bias[e] = (c0 + e < nch && a.bias != nullptr) ? e4::load_scalar(a.bias, cb + c0 + e, a.bias_dtype) : 0.f;
+      bias[e] = a.bias_dtype == EAGLE4_F32    ? __uint_as_float(bias_raw[e])
+                : a.bias_dtype == EAGLE4_BF16 ? e4::bf16_to_f32(static_cast<uint16_t>(bias_raw[e]))
+                                              : e4::f16_to_f32(static_cast<uint16_t>(bias_raw[e]));
     for (int t = tl; t < n; t += kTokLanes) {
       const uint4 xt = xs[t * kVecs + v];
       uint4 win[3];  // parent, grandparent, great-grandparent
@@ -225,7 +245,11 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
           if (a.silu) acc = silu(acc);
           r[k] = acc;
         }
-        o[e / 2] = static_cast<uint32_t>(T::from_f32(r[0])) | static_cast<uint32_t>(T::from_f32(r[1])) << 16;
+        if constexpr (T::code == EAGLE4_BF16) {  // both rounded to nearest even by one instruction
+          asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(o[e / 2]) : "v"(r[0]), "v"(r[1]));
+        } else {
+          o[e / 2] = static_cast<uint32_t>(T::from_f32(r[0])) | static_cast<uint32_t>(T::from_f32(r[1])) << 16;
+        }
       }
       uint16_t* op = out + t * a.stride_o_token + c0 * a.stride_o_dim;
       if (ovec) {
