@@ -309,6 +309,125 @@ E4_DEV void consume_tile(uint32_t stage, const OperandOffsets& off, const u32x4_
   }
 }
 
+// The same step in three phases, for the pipelined consumer loop (16-bit pages): S^T of tile x, then O^T += V^T P^T of
+// tile x - 1 (its P^T kept from the iteration before), then tile x's softmax. The PV products do not depend on tile
+// x's scores, so they run on the matrix core while the softmax runs on the VALU. Same arithmetic, in the same order per
+// accumulator, as consume_tile.
+template <int D, typename T>
+E4_DEV void qk_phase(uint32_t stage, const OperandOffsets& off, const u32x4_t (&q)[D / 32], f32x4_t (&s)[2]) {
+  constexpr int KG = 4;
+  using TL = Tile<D>;
+  constexpr int KB = TL::KB;
+  uint32_t kb[KB];
+#pragma unroll
+  for (int e = 0; e < KB; ++e) kb[e] = stage + off.kb[e];
+  s[0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  s[1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c0 = 0; c0 < D / 32; c0 += KG) {
+    u32x4_t kop[2][KG];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < KG && c0 + c < D / 32; ++c) {
+        const int cc = c0 + c;
+        kop[kt][c] = lds_load16(kb[cc % KB] + 16 * TL::ROWB * kt + 64 * KB * (cc / KB));
+      }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < KG && c0 + c < D / 32; ++c)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) s[kt] = mfma16<T>(kop[kt][c], q[c0 + c], s[kt]);
+  }
+}
+
+template <int D, typename T>
+E4_DEV void pv_phase(uint32_t stage, const OperandOffsets& off, const u32x4_t& pb, f32x4_t (&acc)[D / 16]) {
+  constexpr int VG = 4;
+  using TL = Tile<D>;
+  constexpr int VB = TL::VB;
+  uint32_t vb[VB];
+#pragma unroll
+  for (int v = 0; v < VB; ++v) {
+    vb[v] = off.vb[v];
+    if constexpr (D == 256) {
+      vb[v] += stage;
+      asm volatile("" : "+v"(vb[v]));
+    }
+  }
+  const uint32_t vst = D == 256 ? 0u : stage;
+  auto read_v = [&](int dt) {
+    const uint32_t o = 32 * VB * (dt / VB);
+    const v4i16 lo4 = lds_tr16(vst + vb[dt % VB] + o);
+    const v4i16 hi4 = lds_tr16(vst + vb[dt % VB] + 16 * TL::ROWB + o);
+    return __builtin_shufflevector(__builtin_bit_cast(u32x2_t, lo4), __builtin_bit_cast(u32x2_t, hi4), 0, 1, 2, 3);
+  };
+  u32x4_t vop[VG];
+#pragma unroll
+  for (int i = 0; i < VG && i < D / 16; ++i) vop[i] = read_v(i);
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int d0 = 0; d0 < D / 16; d0 += VG) {
+    u32x4_t nxt[VG];
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) nxt[i] = read_v(d0 + VG + i);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < VG && d0 + i < D / 16; ++i) acc[d0 + i] = mfma16<T>(vop[i], pb, acc[d0 + i]);
+    if (d0 + VG < D / 16) {
+#pragma unroll
+      for (int i = 0; i < VG; ++i) vop[i] = nxt[i];
+    }
+  }
+}
+
+// Tile x's softmax step (consume_tile's): its P^T operand; a raised reference rescales the accumulators, which by
+// then hold tile x - 1's products too (the reference they were computed against is the old one).
+template <int D, typename T>
+E4_DEV u32x4_t softmax_phase(f32x4_t (&s)[2], f32x4_t (&acc)[D / 16], float& mref, float& lsum, float scale_log2,
+                             uint32_t vis, bool full, int g) {
+  constexpr float kSlack = 16.0f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[kt][i] *= scale_log2;
+  if (!full) {
+    asm volatile("");
+    const uint32_t vv = vis >> (4 * g);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[kt][i] = ((vv >> (16 * kt + i)) & 1u) ? s[kt][i] : -INFINITY;
+  }
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, s[kt][i]);
+  if (__any(tmax > mref + kSlack)) {
+    float rm = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
+    const float m_new = fmaxf(mref, rm);
+    const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(mref - m_new);
+    mref = m_new;
+    lsum *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) acc[dt] *= alpha;
+  }
+  const float ref = mref == -INFINITY ? 0.f : mref;
+  uint32_t w[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float p0 = __builtin_amdgcn_exp2f(s[p >> 1][2 * (p & 1)] - ref);
+    const float p1 = __builtin_amdgcn_exp2f(s[p >> 1][2 * (p & 1) + 1] - ref);
+    lsum += p0 + p1;
+    w[p] = pack2<T>(p0, p1);
+  }
+  return u32x4_t{w[0], w[1], w[2], w[3]};
+}
+
 // The consumer step for an fp8 context tile (64 keys, two 32-key halves at K / V + 32 h D): the same schedule over
 // both halves at once — the four S^T chains (half, kt) in flight together, one softmax step over the 64 scores — with
 // the operands widened from fp8 as they are read and the per-(page, KV head) scales folded in per key: into the
@@ -523,6 +642,11 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   constexpr int NS = kStages;
   constexpr int NG = TL::NI / kProducers;  // row groups per producer: nn = producer + kProducers i, K then V
   constexpr int CK = FP8 ? kTileKeys8 : kTileKeys;  // keys of a context tile
+  // Tiles the loads run ahead of the compute: the load of tile x + LD goes out when tile x is handed over. 16-bit pages
+  // run their consumers pipelined (tile x - 1's PV products in iteration x), so stage x - 1 is still read then and the
+  // loads stay two tiles ahead; fp8 pages keep three. Page lookups run NS - 1 tiles ahead of the loads.
+  constexpr bool kPipe = !FP8;
+  constexpr int LD = kPipe ? NS - 2 : NS - 1;
   static_assert(TL::NI % kProducers == 0, "row groups split evenly");
   __shared__ __attribute__((aligned(1024))) char smem[NS][2][TL::BYTES];  // [stage][K, V]
   __shared__ __attribute__((aligned(256))) int s_pid[NS][64];             // page ids of a tile's keys
@@ -805,7 +929,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     __syncthreads();
     static_assert(NS == 4, "the load-count window below is written for four stages");
     int n1 = 0, n2 = 0;  // fp8: direct loads of tiles x + 1 and x + 2 (tiles differ: fp8 context, 16-bit draft)
-    for (int i = 0; i < NS - 1; ++i) {
+    for (int i = 0; i < LD; ++i) {
       int n = 0;
       if (g0 + i < g1) {
         n = loads_of(cd);
@@ -821,7 +945,7 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
     for (int64_t x = g0; x < g1; ++x) {
       const int slot = static_cast<int>(x & (NS - 1));
       const int64_t left = g1 - x - 1;
-      const int later = static_cast<int>(left < NS - 2 ? left : NS - 2);
+      const int later = static_cast<int>(left < LD - 1 ? left : LD - 1);
       if constexpr (FP8) {  // loads issued after tile x's: those of the later tiles and the lookups 4, 5 ahead
         wait_vm_dyn((later >= 1 ? n1 : 0) + (later >= 2 ? n2 : 0) + (pi == 0 ? NS - 2 : 0));
       } else if (pi == 0) {
@@ -829,16 +953,16 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       } else {
         wait_producer<NS, 2 * NG, 0>(later);
       }
-      __syncthreads();  // tile x is in LDS; stage x - 1 has been read by every consumer
+      __syncthreads();  // tile x is in LDS; stage x - LD + 1 ... x - 1 ... has been read by every consumer
       int n3 = 0;
-      if (x + NS - 1 < g1) {
+      if (x + LD < g1) {
         n3 = loads_of(cd);
-        load_tile(cd, (slot + NS - 1) & (NS - 1));
+        load_tile(cd, (slot + LD) & (NS - 1));
       }
       n1 = n2;
       n2 = n3;
       cur_next<CK>(cd, s_qsl, s_ctx, B, HR);
-      lookup(cl, (slot + 2 * NS - 2) & (NS - 1));
+      lookup(cl, (slot + LD + NS - 1) & (NS - 1));
       cur_next<CK>(cl, s_qsl, s_ctx, B, HR);
     }
     wait_vm<0>();
@@ -889,13 +1013,17 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
   Cursor cn = cc;
   // tiles whose keys are all visible skip the mask (at D 256; smaller heads have no registers to spare for it)
   constexpr bool kFullTiles = D == 256;
+  // pipelined consumers: tile x - 1's P^T and stage, its PV products still to run
+  bool pend = false;
+  int prev = 0;
+  u32x4_t pb = {0u, 0u, 0u, 0u};
   // the first rows' loads waited for here, so that the loop's wait for a segment's rows (loaded before the previous
   // piece's stores) is not merged with a wait made for these
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) asm volatile("" ::"v"(q[i]));
   asm volatile("" ::"v"(row_mask));
 #pragma unroll
-  for (int i = 0; i < NS; ++i) __syncthreads();  // the producers' prologue
+  for (int i = 0; i < LD + 1; ++i) __syncthreads();  // the producers' prologue
 
   for (int64_t x = g0; x < g1; ++x) {
     const int slot = static_cast<int>(x & (NS - 1));
@@ -917,6 +1045,14 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
                              visible(false, base + 32, cc.ctx, cc.width, row_mask),
                              kFullTiles && base + kTileKeys8 <= cc.ctx, g,
                              reinterpret_cast<const float4*>(s_scl[FP8 ? slot : 0]));
+    } else if constexpr (kPipe) {
+      f32x4_t sx[2];
+      qk_phase<D, T>(lds_addr(smem[slot][0]), off, q, sx);
+      if (pend) pv_phase<D, T>(lds_addr(smem[prev][0]), off, pb, acc);  // tile x - 1's, behind the QK products
+      pb = softmax_phase<D, T>(sx, acc, mref, lsum, scale_log2, visible(is_new, base, cc.ctx, cc.width, row_mask),
+                               kFullTiles && !is_new && base + kTileKeys <= cc.ctx, g);
+      pend = true;
+      prev = slot;
     } else {
       consume_tile<D, T>(lds_addr(smem[slot][0]), off, q, acc, mref, lsum, scale_log2,
                          visible(is_new, base, cc.ctx, cc.width, row_mask),
@@ -931,6 +1067,10 @@ void verify_stream_kernel(const eagle4_attn_args a, const StreamPlan p) {
       if (seg_end) seg_w[1] = w;
     }
     if (seg_end || x == g1 - 1) {
+      if constexpr (kPipe) {  // the piece's last PV products
+        pv_phase<D, T>(lds_addr(smem[slot][0]), off, pb, acc);
+        pend = false;
+      }
       const bool more = x + 1 < g1;
       float ls = lsum + __shfl_xor(lsum, 16, 64);
       ls += __shfl_xor(ls, 32, 64);
