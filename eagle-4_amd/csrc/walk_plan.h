@@ -8,9 +8,13 @@
 //
 // Built in parallel rather than by loops over the rows: child masks and first children by LDS atomics, depths and
 // the successor's ancestor by pointer jumping over lane shuffles, needs one tree level at a time (children of the
-// level below already counted into a per-row histogram). A serial row loop costs ~100 ns per row in one wave (a
-// readlane, scalar branches and the vector updates per step), ~5 us for a 16-row tree.
+// level below already counted into a per-row histogram), from the deepest level present. A serial row loop costs
+// ~100 ns per row in one wave (a readlane, scalar branches and the vector updates per step), ~5 us for a 16-row tree;
+// for the needs alone, a pass over 16 rows in decreasing index with lane-held histograms took 1.6 us against 1.3 for
+// the levels.
 #pragma once
+
+#include <utility>
 
 #include "common.h"
 
@@ -40,10 +44,27 @@ E4_DEV int plan_next(int pl) { return (pl & kNoNext) == kNoNext ? -1 : (pl & kNo
 // has to stop the compiler from moving them.
 E4_DEV void wave_lds_order() { __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront"); }
 
+// One rotation of the repeat check within each 16-lane row (DPP row_ror: no LDS round trip): lane u compares its slot
+// with that of the lane D places along its row, whose index comes along the same rotation.
+template <int D>
+E4_DEV void row_repeat(int lo, int lane, int T, bool& dup) {
+  const int other = __builtin_amdgcn_mov_dpp(lo, 0x120 + D, 0xF, 0xF, false);
+  const int from = __builtin_amdgcn_mov_dpp(lane, 0x120 + D, 0xF, 0xF, false);
+  dup = dup || (lane < T && from < T && other == lo);
+}
+template <int... Ds>
+E4_DEV bool row_repeats(int lo, int lane, int T, std::integer_sequence<int, Ds...>) {
+  bool dup = false;
+  (row_repeat<Ds + 1>(lo, lane, T, dup), ...);
+  return dup;
+}
+
 // Lane u: whether row u's 64-bit slot equals another row's, compared on the low words. Equal low words with different
 // high words also count: a request with a duplicate keeps the index-order walk, which is exact for any slots.
+// At most 16 rows all sit in the wave's first row of 16 lanes: 15 rotations within it; more rows, lane shuffles.
 E4_DEV bool slot_repeats(uint64_t slot, int lane, int T) {
   const int lo = static_cast<int>(static_cast<uint32_t>(slot));
+  if (T <= 16) return row_repeats(lo, lane, T, std::make_integer_sequence<int, 15>{});
   bool dup = false;
 #pragma unroll 4
   for (int d = 1; d < T; ++d) {  // row u against row (u + d) mod 64: every pair of rows once per direction
@@ -88,7 +109,13 @@ E4_DEV int build_plan(PlanScratch& ps, int lane, int T, int par, bool by_need) {
       up = u2;
     }
     // the deepest level first: a row's children (one level down) have all counted themselves into its histogram
-    for (int level = T - 1; level >= 1; --level) {
+    int deepest = 0;  // the deepest level, bit by bit from ballots (depths are below 64)
+#pragma unroll
+    for (int b = 5; b >= 0; --b) {
+      const int cand = deepest | (1 << b);
+      if (__ballot(lane < T && dep >= cand) != 0) deepest = cand;
+    }
+    for (int level = deepest; level >= 1; --level) {
       const bool mine = child && dep == level;
       if (__ballot(mine) == 0) continue;
       if (mine) {

@@ -56,7 +56,11 @@ def emulate_build_plan(parents: list[int], by_need: bool) -> list[int]:
             d2, u2 = dep[up], up[up]
             dep = dep + d2
             up = u2
-        for level in range(T - 1, 0, -1):  # the deepest level first
+        deepest = 0  # bit by bit from ballots
+        for b in range(5, -1, -1):
+            if np.any((lane < T) & (dep >= (deepest | (1 << b)))):
+                deepest |= 1 << b
+        for level in range(deepest, 0, -1):  # the deepest level first
             mine = child & (dep == level)
             if not mine.any():
                 continue
