@@ -83,7 +83,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   auto& s_kr = *reinterpret_cast<IS(*)[TS][K]>(s_stack + TS * K * sizeof(IS));
   // The walk plan's scratch while wave 0 builds it and hands it over: in s_q, which is first written after the
   // staged rows are normalised, where it fits.
-  constexpr bool kPlanInQ = sizeof(float) * TS * K >= sizeof(PlanScratch);
+  // (At 16 lanes per row, the small grids, the plan has LDS of its own, so the norms write q^ and k^ at once.)
+  constexpr bool kPlanInQ = C < 16 && sizeof(float) * TS * K >= sizeof(PlanScratch);
   __shared__ __align__(16) char s_plan_own[kPlanInQ ? 16 : sizeof(PlanScratch)];
   PlanScratch& ps = *reinterpret_cast<PlanScratch*>(kPlanInQ ? reinterpret_cast<char*>(&s_q[0][0]) : s_plan_own);
 
@@ -174,13 +175,17 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __syncthreads();
   const int plan = ps.plan[lane];  // read before s_q is written, after the next barrier
   const bool dfs = ps.dfs != 0;
-  stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
-  __syncthreads();
-  for (int i = tid; i < ts * K; i += NT) {  // q^ and k^, read by every node of the walk
-    const int t = i / K, e = i % K;
-    const float4 sc = s_sc[t];
-    s_q[t][e] = Tin::to_f32(s_qr[t][e]) * sc.z;
-    s_k[t][e] = Tin::to_f32(s_kr[t][e]) * sc.w;
+  if constexpr (kPlanInQ) {
+    stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
+    __syncthreads();
+    for (int i = tid; i < ts * K; i += NT) {  // q^ and k^, read by every node of the walk
+      const int t = i / K, e = i % K;
+      const float4 sc = s_sc[t];
+      s_q[t][e] = Tin::to_f32(s_qr[t][e]) * sc.z;
+      s_k[t][e] = Tin::to_f32(s_kr[t][e]) * sc.w;
+    }
+  } else {  // the norms and q^, k^ in one pass (s_q does not hold the plan)
+    stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale, s_q, s_k);
   }
   __syncthreads();  // the raw rows' space becomes the stack
 

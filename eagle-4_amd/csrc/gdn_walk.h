@@ -255,29 +255,41 @@ struct Staging {
 
 // L2 norms over K of the staged nodes (kernels/gdn_tree_recurrence.py:143-151), all nodes at once: NT / TS
 // adjacent threads share a node, each summing a contiguous run of its q and k; .z = scale / |q|, .w = 1 / |k|
-// (1e-6 inside the square roots).
+// (1e-6 inside the square roots). With qh / kh, every thread also writes its run of q^ = q .z and k^ = k .w there
+// (the same products the separate pass makes), so no second pass over the raw rows follows.
 template <typename Tin, int K, int TS, int NT>
 E4_DEV void stage_norms(const typename Tin::storage (&s_q)[TS][K], const typename Tin::storage (&s_k)[TS][K],
-                        float4 (&s_sc)[TS], int ts, int tid, float scale) {
+                        float4 (&s_sc)[TS], int ts, int tid, float scale, float (*qh)[K] = nullptr,
+                        float (*kh)[K] = nullptr) {
   constexpr int LPN0 = NT / TS < 64 ? NT / TS : 64;
   constexpr int LPN = LPN0 < K ? LPN0 : K;  // threads per node (a power of two)
   constexpr int PER = K / LPN;                       // elements each
   static_assert(PER >= 1 && K % LPN == 0, "norm split");
   const int t = tid / LPN, part = tid % LPN;
   float qq = 0.f, kk = 0.f;
+  float qv[PER], kv[PER];
   if (t < ts) {
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
-      const float qv = Tin::to_f32(s_q[t][part * PER + e]), kv = Tin::to_f32(s_k[t][part * PER + e]);
-      qq = fmaf(qv, qv, qq);
-      kk = fmaf(kv, kv, kk);
+      qv[e] = Tin::to_f32(s_q[t][part * PER + e]);
+      kv[e] = Tin::to_f32(s_k[t][part * PER + e]);
+      qq = fmaf(qv[e], qv[e], qq);
+      kk = fmaf(kv[e], kv[e], kk);
     }
   }
   qq = e4::group_sum<LPN>(qq);
   kk = e4::group_sum<LPN>(kk);
+  const float qs = scale / sqrtf(qq + 1e-6f), ks = 1.0f / sqrtf(kk + 1e-6f);
   if (t < ts && part == 0) {
-    s_sc[t].z = scale / sqrtf(qq + 1e-6f);
-    s_sc[t].w = 1.0f / sqrtf(kk + 1e-6f);
+    s_sc[t].z = qs;
+    s_sc[t].w = ks;
+  }
+  if (qh != nullptr && t < ts) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      qh[t][part * PER + e] = qv[e] * qs;
+      kh[t][part * PER + e] = kv[e] * ks;
+    }
   }
 }
 
