@@ -78,15 +78,15 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   __shared__ __align__(16) float s_k[TS][K];
   __shared__ IS s_v[TS][ROWS];
   __shared__ float4 s_sc[TS];  // decay, beta, scale / |q|, 1 / |k|
-  __shared__ float s_out[TS][ROWS];  // the staged nodes' outputs, stored in one pass after the walk
+  __shared__ __align__(16) float s_out[TS][ROWS];  // the staged nodes' outputs, stored in one pass after the walk
   auto& s_qr = *reinterpret_cast<IS(*)[TS][K]>(s_stack);
   auto& s_kr = *reinterpret_cast<IS(*)[TS][K]>(s_stack + TS * K * sizeof(IS));
-  // The walk plan's scratch while wave 0 builds it and hands it over: in s_q, which is first written after the
-  // staged rows are normalised, where it fits.
-  // (At 16 lanes per row, the small grids, the plan has LDS of its own, so the norms write q^ and k^ at once.)
-  constexpr bool kPlanInQ = C < 16 && sizeof(float) * TS * K >= sizeof(PlanScratch);
-  __shared__ __align__(16) char s_plan_own[kPlanInQ ? 16 : sizeof(PlanScratch)];
-  PlanScratch& ps = *reinterpret_cast<PlanScratch*>(kPlanInQ ? reinterpret_cast<char*>(&s_q[0][0]) : s_plan_own);
+  // The walk plan's scratch while wave 0 builds it and hands it over: in s_out, first written by the walk itself,
+  // where it fits (16-bit inputs at 32 rows per workgroup), else LDS of its own; s_q stays free, so the staged rows'
+  // norms write q^ and k^ in the same pass.
+  constexpr bool kPlanInOut = sizeof(float) * TS * ROWS >= sizeof(PlanScratch);
+  __shared__ __align__(16) char s_plan_own[kPlanInOut ? 16 : sizeof(PlanScratch)];
+  PlanScratch& ps = *reinterpret_cast<PlanScratch*>(kPlanInOut ? reinterpret_cast<char*>(&s_out[0][0]) : s_plan_own);
 
   int n, hv, tile;
   item_of(blockIdx.x, a.HV, (a.V + ROWS - 1) / ROWS, n, hv, tile);
@@ -173,20 +173,10 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
 #pragma unroll
     for (int j = 0; j < NJ; ++j) widen_state_raw(h0raw[s][j], a.h0_dtype, &h[s][4 * j]);
   __syncthreads();
-  const int plan = ps.plan[lane];  // read before s_q is written, after the next barrier
+  const int plan = ps.plan[lane];  // read before the walk writes s_out (after the next barrier)
   const bool dfs = ps.dfs != 0;
-  if constexpr (kPlanInQ) {
-    stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale);  // L2 norms over K (:143-151)
-    __syncthreads();
-    for (int i = tid; i < ts * K; i += NT) {  // q^ and k^, read by every node of the walk
-      const int t = i / K, e = i % K;
-      const float4 sc = s_sc[t];
-      s_q[t][e] = Tin::to_f32(s_qr[t][e]) * sc.z;
-      s_k[t][e] = Tin::to_f32(s_kr[t][e]) * sc.w;
-    }
-  } else {  // the norms and q^, k^ in one pass (s_q does not hold the plan)
-    stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale, s_q, s_k);
-  }
+  // L2 norms over K (:143-151) and q^, k^ (read by every node of the walk) in one pass
+  stage_norms<Tin, K, TS, NT>(s_qr, s_kr, s_sc, ts, tid, a.scale, s_q, s_k);
   __syncthreads();  // the raw rows' space becomes the stack
 
   settle_loads();  // the initial state and the plan tables
