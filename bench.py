@@ -14,7 +14,8 @@ A step is one pass of the hot path over one batch of synthetic input, resident i
 roofline (algorithmic HBM bytes per launch / its HIP-event duration, against MI355X's 8 TB/s), the CPU baseline
 (the oracle, timed on a bounded sample on this host's cores) and the records contract's chunk form per layer at
 1 / 4 / 16 / 32 requests beside the reference's published times (``--records-only`` prints just that). ``--calibrate-copy`` instead times a plain 1 GiB
-device copy (the reference kernel for the rocprofv3 FETCH_SIZE / WRITE_SIZE scale).
+device copy (the reference kernel for the rocprofv3 FETCH_SIZE / WRITE_SIZE scale) and a 2 GiB fill (the write
+ceiling).
 """
 
 from __future__ import annotations
@@ -715,6 +716,19 @@ def _calibrate_copy(steps: int) -> None:
     dt = (time.perf_counter() - t0) / steps
     print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "ms": dt * 1e3,
                       "GB/s (read+write)": 2 * n / dt / 1e9}), flush=True)
+    # the write ceiling: a 2 GiB fill (the GDN walk's snapshot stores are ~2.2 GB of writes per step)
+    big = torch.empty(2 * n // 4, dtype=torch.float32, device=dev)
+    del src, dst
+    for _ in range(2):
+        big.fill_(1.0)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        big.fill_(1.0)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    print(json.dumps({"calibration": "device fill", "bytes_written": 2 * n, "ms": dt * 1e3,
+                      "GB/s (write)": 2 * n / dt / 1e9}), flush=True)
 
 
 def main() -> int:
