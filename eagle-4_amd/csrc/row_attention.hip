@@ -6,14 +6,17 @@
 //
 // One workgroup per (key split, KV head and group of 64 rows, request): a row is (row of the request, query head of
 // the KV head's group), so one read of each key serves all the rows of all G query heads (the reference's grid is per
-// query head and reads every key G times). 32-key tiles of K and V go straight from HBM into a double-buffered LDS
-// tile (global_load_lds, the verify attention's swizzled layout) one tile ahead, their slots looked up two tiles
-// ahead; each wave runs the verify
-// attention's tile step (S^T = K Q^T and O^T = V^T P^T on the 16x16x32 MFMA, online softmax in the log2 domain) for
-// its 16 rows with a per-row key range. A draft step's ancestors are one more split. Every split leaves an fp32
+// query head and reads every key G times). 32-key tiles of K and V go straight from HBM into a three-stage LDS ring
+// (global_load_lds, the verify attention's swizzled layout) two tiles ahead, their slots looked up (page-table entries
+// or ancestor slots, also loaded straight into LDS) two tiles further ahead; with three workgroups per CU and, at a
+// draft step's 16 rows per KV head, one wave of four computing, a double buffer one tile ahead held too few bytes in
+// flight (3.9 TB/s). Each wave runs the verify attention's tile step (S^T = K Q^T and O^T = V^T P^T on the 16x16x32
+// MFMA, online softmax in the log2 domain) for its 16 rows with a per-row key range. A draft step's ancestors are one more split. Every split leaves an fp32
 // partial and its log2-sum-exp in the caller's scratch; a second kernel merges them (:213-240).
 
 #include "attention_tile.h"
+
+#pragma clang diagnostic ignored "-Winline-asm"  // the direct loads set M0; no compiler-generated code here uses M0
 
 namespace {
 
@@ -21,6 +24,23 @@ using namespace e4attn;
 
 constexpr int NW = 4;  // waves per workgroup: 64 rows
 constexpr int NT = 64 * NW;
+constexpr int kRing = 3;  // LDS stages of the streamed path
+
+E4_DEV uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)p));
+}
+
+// 64 lanes x 16 bytes from per-lane global addresses into LDS [lds, lds + 1024), lane p at lds + 16 p, read once
+// (nontemporal).
+E4_DEV void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+template <int N>
+E4_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // First key position a query at `pos` sees (window <= 0: the whole context) (:75-81).
 E4_DEV int64_t window_start(int64_t pos, int window) {
@@ -33,7 +53,7 @@ template <int D, typename T>
 __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn_args a, int groups) {
   using TL = Tile<D>;
   constexpr int CH = D / 8;                      // 16-byte chunks per key row
-  __shared__ __attribute__((aligned(1024))) char smem[2][2][TL::BYTES];  // [buffer][K, V]
+  __shared__ __attribute__((aligned(1024))) char smem[kRing][2][TL::BYTES];  // [stage][K, V]
 
   const int split = blockIdx.x, kvh = blockIdx.y / groups, grp = blockIdx.y % groups, b = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, l16 = lane & 15;
@@ -87,50 +107,54 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
   const int cp_shift = (a.cache_page & (a.cache_page - 1)) == 0 ? __builtin_ctz(a.cache_page) : -1;
   // Direct loads (global_load_lds): instruction n of a tile fills 1 KB run n of the LDS tile, lane p its 16-byte slot
   // p — row n * RPI + p / CH, the chunk the tile's swizzle puts at slot p % CH. Wave w issues instructions
-  // n = w + NW m. A lane's rows are looked up (page table or ancestor list) two tiles ahead, so the lookup's latency
-  // hides behind a tile, and the tile's K / V load one tile ahead into the other LDS buffer.
+  // n = w + NW i. Per tile a wave issues one lookup — lane j < NIW RPI loads the page-table entry (or the ancestor's
+  // KV slot) of row j of its instructions straight into LDS — and, two tiles later, its K and V loads from per-lane
+  // addresses built from those entries; the loads run two tiles ahead of the compute through a three-stage ring.
+  // Lookups and loads are issued from inline assembly and waited for by count (vector memory operations retire in
+  // issue order): the compiler, which would wait for every load before the tile step's first LDS read, sees neither.
   constexpr int RPI = TL::RPI, NI = TL::NI, NIW = NI / NW;
-  static_assert(NI % NW == 0, "instructions per wave");
-  uint32_t raw[NIW], rem[NIW];  // page-table entry and position within the page (or the ancestor's KV slot)
-  auto lookup = [&](int tile) {
-    const int64_t base = start + static_cast<int64_t>(tile) * kTileKeys;
-#pragma unroll
-    for (int i = 0; i < NIW; ++i) {
-      const int row = (wave + NW * i) * RPI + lane / CH;
-      const int64_t c = base + row < end ? base + row : end - 1;  // past the split: its last key (masked later)
-      if (anc) {
-        const int owner = static_cast<int>(c / a.max_depth), dep = static_cast<int>(c % a.max_depth);
-        // owner < rows_per_request: the split ends at rows * max_depth. A column past the row's `step` ancestors
-        // loads the row's first ancestor instead (written: the split exists only for step >= 1), so the masked key
-        // multiplies finite data, never a slot nobody wrote
-        const bool valid = dep < a.step;
-        raw[i] = static_cast<uint32_t>(
-            a.ancestors[(static_cast<int64_t>(b) * a.rows_per_request + owner) * a.max_depth + (valid ? dep : 0)]);
-        rem[i] = 0;  // unused by the ancestor split; defined on both paths (left undefined, 12 registers spilled)
-      } else {
-        const uint32_t pos = static_cast<uint32_t>(c), tp = static_cast<uint32_t>(a.table_page);
-        const uint32_t pg = tp_shift >= 0 ? pos >> tp_shift : pos / tp;
-        raw[i] = static_cast<uint32_t>(table[pg]);
-        rem[i] = pos - pg * tp;
-      }
-    }
+  static_assert(NI % NW == 0 && NIW * RPI <= 64, "instructions per wave");
+  __shared__ int32_t s_ent[4][NW][64];  // a ring of four tiles' lookups per wave
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  auto key_of = [&](int tile, int row) {  // the key a tile row loads: past the split, the split's last key (masked)
+    const int64_t c = start + static_cast<int64_t>(tile) * kTileKeys + row;
+    return c < end ? c : end - 1;
   };
-  auto issue = [&](int tile) {
-    char* const kb = smem[tile & 1][0];
-    char* const vb = smem[tile & 1][1];
+  auto lookup = [&](int tile) {
+    const int j = lane < NIW * RPI ? lane : 0;
+    const int64_t c = key_of(tile, (wv + NW * (j / RPI)) * RPI + j % RPI);
+    const int32_t* src;
+    if (anc) {
+      // owner < rows_per_request: the split ends at rows * max_depth. A column past the row's `step` ancestors
+      // loads the row's first ancestor instead (written: the split exists only for step >= 1), so the masked key
+      // multiplies finite data, never a slot nobody wrote
+      const int ci = static_cast<int>(c), owner = ci / a.max_depth, dep = ci - owner * a.max_depth;
+      src = a.ancestors + (static_cast<int64_t>(b) * a.rows_per_request + owner) * a.max_depth + (dep < a.step ? dep : 0);
+    } else {
+      const uint32_t pos = static_cast<uint32_t>(c), tp = static_cast<uint32_t>(a.table_page);
+      src = table + (tp_shift >= 0 ? pos >> tp_shift : pos / tp);
+    }
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src),
+                 "s"(lds_addr(&s_ent[tile & 3][wv][0])) : "memory", "m0");
+  };
+  auto issue = [&](int tile, int stage) {
+    const uint32_t kl = lds_addr(smem[stage][0]), vl = lds_addr(smem[stage][1]);
 #pragma unroll
     for (int i = 0; i < NIW; ++i) {
-      const int n = wave + NW * i, row = n * RPI + lane / CH, pc = lane % CH;
-      const uint32_t slot = anc ? raw[i] : raw[i] * static_cast<uint32_t>(a.table_page) + rem[i];
+      const int n = wv + NW * i, row = n * RPI + lane / CH, pc = lane % CH;
+      const uint32_t ent = static_cast<uint32_t>(s_ent[tile & 3][wv][i * RPI + lane / CH]);
+      uint32_t slot = ent;
+      if (!anc) {
+        const uint32_t pos = static_cast<uint32_t>(key_of(tile, row)), tp = static_cast<uint32_t>(a.table_page);
+        const uint32_t pg = tp_shift >= 0 ? pos >> tp_shift : pos / tp;
+        slot = ent * tp + (pos - pg * tp);
+      }
       const uint32_t cpg = static_cast<uint32_t>(a.cache_page);
       const uint32_t blk = cp_shift >= 0 ? slot >> cp_shift : slot / cpg, in = slot - blk * cpg;
       const int64_t koff = 2 * (blk * a.k_stride_page + in * a.k_stride_slot + kvh * a.k_stride_head);
       const int64_t voff = 2 * (blk * a.v_stride_page + in * a.v_stride_slot + kvh * a.v_stride_head + voff_packed);
-      // the builtin takes its source as a plain pointer variable
-      const char* ksrc = kc + koff + 16 * (pc ^ TL::kswz(row));
-      const char* vsrc = vc + voff + 16 * (pc ^ TL::vswz(row));
-      __builtin_amdgcn_global_load_lds(ksrc, kb + n * 1024, 16, 0, 2);
-      __builtin_amdgcn_global_load_lds(vsrc, vb + n * 1024, 16, 0, 2);
+      dma16(kc + koff + 16 * (pc ^ TL::kswz(row)), kl + n * 1024);
+      dma16(vc + voff + 16 * (pc ^ TL::vswz(row)), vl + n * 1024);
     }
   };
 
@@ -140,21 +164,38 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
   float m = -INFINITY, l = 0.f;
   const float scale_log2 = a.scale * 1.4426950408889634f;
   const bool wave_rows = (grp * NW + wave) * 16 < R;  // a wave without rows loads, but skips the math
-  if (ntiles > 0) {
-    lookup(0);
-    issue(0);
-    if (ntiles > 1) lookup(1);
-  }
+  // prologue: the lookups of tiles 0 .. 3, then the loads of tiles 0 and 1
+  constexpr int TL2 = 2 * NIW;  // loads per tile and wave
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+    if (x < ntiles) lookup(x);
+  // the lookups, and q: a wait the compiler sees, so that it places none of its own for q inside the loop (there it
+  // would drain the ring)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  if (ntiles > 0) issue(0, 0);
+  if (ntiles > 1) issue(1, 1);
+  int stage = 0;
   for (int x = 0; x < ntiles; ++x) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // tile x's loads (issued a tile ago) have landed, lookups too
-    __syncthreads();  // ... for every wave, and the other buffer is no longer read
-    if (x + 1 < ntiles) {
-      issue(x + 1);
-      if (x + 2 < ntiles) lookup(x + 2);
+    // Issued after tile x's loads: the lookup of x + 2 (from x = 2; before, the prologue's, already waited for),
+    // then the loads of x + 1 and the lookup of x + 3 (from x = 1). Waiting until only the last two groups are
+    // outstanding lands tile x's loads and the lookup of x + 2.
+    const int newer = (x + 1 < ntiles ? TL2 : 0) + (x >= 1 && x + 3 < ntiles ? 1 : 0);
+    if (newer == TL2 + 1)
+      wait_vm<TL2 + 1>();
+    else if (newer == TL2)
+      wait_vm<TL2>();
+    else if (newer == 1)
+      wait_vm<1>();
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // ... for every wave, and stage x - 1 is no longer read
+    if (x + 2 < ntiles) {
+      issue(x + 2, stage == 0 ? kRing - 1 : stage - 1);
+      if (x + 4 < ntiles) lookup(x + 4);
     }
     if (wave_rows) {
       const int64_t base = start + static_cast<int64_t>(x) * kTileKeys;
-      tile_step_if<D, T>(smem[x & 1][0], smem[x & 1][1], qreg, acc, m, l, scale_log2, g, l16, [&](int k) {
+      tile_step_if<D, T>(smem[stage][0], smem[stage][1], qreg, acc, m, l, scale_log2, g, l16, [&](int k) {
         const int64_t c = base + k;
         if (!row_ok || c >= end) return false;
         const int64_t own = static_cast<int64_t>(t) * a.max_depth;  // a row's own ancestor columns
@@ -162,6 +203,7 @@ __global__ __launch_bounds__(NT) void row_attention_kernel(const eagle4_row_attn
         return c >= lo && c <= hi;
       });
     }
+    stage = stage == kRing - 1 ? 0 : stage + 1;
   }
 
   // the split's partial of this row (:186-199): out / denominator and the log2-sum-exp
