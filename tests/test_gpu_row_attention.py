@@ -110,6 +110,29 @@ def test_gqa_packed_paged_cache(dev, step, D, dtype):
     _check(got, q, cache, None, table, seq, anc, rows_per_request=rows, step=step, window=512, table_page=tpage)
 
 
+@pytest.mark.parametrize("length", [17, 33, 64, 65, 97, 129, 161, 200])
+@pytest.mark.parametrize("step", [0, 9])
+def test_every_ring_depth_of_a_split(dev, length, step):
+    """One split over the whole context, so the split's tile count is ceil(length / 32): 1 .. 7 tiles take every
+    prologue and wait count of the kernel's three-stage ring (loads two tiles ahead, lookups two further). At step 9
+    the ancestors' split holds 16 rows x 12 columns (6 tiles); the table is paged (16 slots per entry)."""
+    announce(f"row attention ring depths length={length} step={step}")
+    rows, depth, heads, D, tpage = (16, 12, 4, 128, 16) if step else (8, 1, 4, 128, 16)
+    gen = torch.Generator(device=dev).manual_seed(length * 10 + step)
+    nslots = 64 * tpage
+    table = torch.randperm(64, device=dev, generator=gen).to(torch.int32).view(2, 32)
+    req = torch.tensor([1], dtype=torch.int64, device=dev)
+    seq = torch.tensor([length], device=dev)
+    k = torch.randn(nslots, heads, D, device=dev, generator=gen).bfloat16()
+    v = torch.randn(nslots, heads, D, device=dev, generator=gen).bfloat16()
+    q = torch.randn(rows, heads, D, device=dev, generator=gen).bfloat16()
+    anc = torch.randint(0, nslots, (1, rows, depth), dtype=torch.int32, device=dev, generator=gen) if step else None
+    kw = dict(rows_per_request=rows, step=step, window=0, table_rows=req, table_page=tpage)
+    got = _run(dev, q, k, v, table, seq, anc, rows=rows, step=step, window=0, splits=1, table_rows=req,
+               table_page=tpage)
+    _check(got, q, k, v, table, seq, anc, **kw)
+
+
 @pytest.mark.parametrize("step", [1, 4])
 def test_masked_ancestor_columns_read_no_unwritten_slot(dev, step):
     """A draft step's ancestor split has max_depth columns per row, of which the first ``step`` are the row's
