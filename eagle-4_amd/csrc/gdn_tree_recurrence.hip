@@ -144,10 +144,13 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
                        a.h0_dtype, h0raw[s][j]);
     }
   const int ts = T < TS ? T : TS;
-  Staging<Tin, K, TS, ROWS, NT> stg;
+  // Waves 1 .. WAVES - 1 stage the nodes while wave 0 builds the walk plan, so wave 0 goes from its plan straight to
+  // the barrier (batch 1: the plan is the prologue's longest path)
+  static_assert(WAVES >= 2, "a plan wave and staging waves");
+  Staging<Tin, K, TS, ROWS, NT - 64> stg;
   const NodeSrc src{a.q, a.k, a.v, a.a, a.b, a.stride_q, a.stride_k, a.stride_v, a.stride_a, a.stride_b,
                     a.gate_dtype, ih, hv, a.V};
-  stg.issue(src, bos, ts, row0, tid);
+  if (wave > 0) stg.issue(src, bos, ts, row0, tid - 64);
 
   // The walk plan (walk_plan.h), built by wave 0 and read by every wave after the staging barrier. Depth first needs
   // reloads that return the parent's own snapshot: parents before children, every row a real slot, no two rows one.
@@ -167,7 +170,8 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   // ---- staging: q, k, v and the node scalars of nodes [0, ts) into LDS --------------------------------------------
   const float A = -expf(widen_raw(A_raw, a.A_log_dtype));
   const float dt_bias = widen_raw(dt_raw, a.dt_bias_dtype);
-  stg.commit(s_qr, s_kr, s_v, s_sc, ts, tid, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
+  if (wave > 0)
+    stg.commit(s_qr, s_kr, s_v, s_sc, ts, tid - 64, a.gate_dtype, a.softplus_beta, a.softplus_threshold, A, dt_bias);
 #pragma unroll
   for (int s = 0; s < RPT; ++s)
 #pragma unroll
