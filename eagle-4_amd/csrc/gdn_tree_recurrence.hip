@@ -70,6 +70,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   using SS = typename Tsnap::storage;
   constexpr int TS = sizeof(IS) == 4 ? 8 : 16;  // staged nodes
   constexpr bool kExact = sizeof(SS) == 4;      // fp32 snapshots: a reload gives the registers bit for bit
+  constexpr bool kFastWalk = E <= 8;            // the depth-first walk of staged nodes has a loop of its own
   // The parked-state stack; in the prologue, before any state is parked, it holds the staged nodes' raw q and k rows.
   constexpr int kStackBytes = WAVES * S * RPT * NJ * 64 * 16;
   constexpr int kRawBytes = 2 * TS * K * static_cast<int>(sizeof(IS));
@@ -188,20 +189,23 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   // address is one readlane and an add
   const int64_t my_off = my_slot > a.pad_slot_id ? my_slot * a.stride_snap_slot + lane * a.stride_snap_row : -1;
   // A node's inputs: staged nodes from LDS, later ones (T > TS) from global memory with their scalars computed here.
+  auto fetch_staged = [&](NodeIn<E, RPT, IS>& nd, int u) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const float4 q4 = *reinterpret_cast<const float4*>(&s_q[u][4 * c + 4 * C * j]);
+      const float4 k4 = *reinterpret_cast<const float4*>(&s_k[u][4 * c + 4 * C * j]);
+      nd.q[4 * j] = q4.x, nd.q[4 * j + 1] = q4.y, nd.q[4 * j + 2] = q4.z, nd.q[4 * j + 3] = q4.w;
+      nd.k[4 * j] = k4.x, nd.k[4 * j + 1] = k4.y, nd.k[4 * j + 2] = k4.z, nd.k[4 * j + 3] = k4.w;
+    }
+#pragma unroll
+    for (int s = 0; s < RPT; ++s) nd.v[s] = s_v[u][lrow[s]];
+    const float4 sc = s_sc[u];
+    nd.decay = sc.x;
+    nd.beta = sc.y;
+  };
   auto fetch = [&](NodeIn<E, RPT, IS>& nd, int u) {
     if (u < TS) {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const float4 q4 = *reinterpret_cast<const float4*>(&s_q[u][4 * c + 4 * C * j]);
-        const float4 k4 = *reinterpret_cast<const float4*>(&s_k[u][4 * c + 4 * C * j]);
-        nd.q[4 * j] = q4.x, nd.q[4 * j + 1] = q4.y, nd.q[4 * j + 2] = q4.z, nd.q[4 * j + 3] = q4.w;
-        nd.k[4 * j] = k4.x, nd.k[4 * j + 1] = k4.y, nd.k[4 * j + 2] = k4.z, nd.k[4 * j + 3] = k4.w;
-      }
-#pragma unroll
-      for (int s = 0; s < RPT; ++s) nd.v[s] = s_v[u][lrow[s]];
-      const float4 sc = s_sc[u];
-      nd.decay = sc.x;
-      nd.beta = sc.y;
+      fetch_staged(nd, u);
     } else {
       const int64_t tok = bos + u;
       const IS* q = static_cast<const IS*>(a.q) + tok * a.stride_q + static_cast<int64_t>(ih) * K;
@@ -259,147 +263,193 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   float4 (*const my_stack)[RPT * NJ][64] = reinterpret_cast<float4 (*)[S][RPT * NJ][64]>(s_stack)[wave];
   const bool full_tile = row0 + ROWS <= a.V;  // every row of the tile exists: stores need no row predicate
 
-  NodeIn<E, RPT, IS> cur, nxt;
-  fetch(cur, 0);
-  int u = 0, sp = 0;
-  uint64_t unparked = 0;  // nodes with several children that found the stack full
-  for (int it = 0; it < T; ++it) {
-    // the next node and where its state comes from
-    int next = -1, pl = 0;
-    if (dfs) {
-      pl = readlane(plan, u);
-      next = plan_next(pl);
-      if (next >= T) next = -1;  // (never: plan rows are the request's)
-    } else if (u + 1 < T) {
-      next = u + 1;
-    }
-    const bool next_first = (pl & kPlanFirst) != 0, next_last = (pl & kPlanLast) != 0;
-    if (next >= 0 && next < TS) fetch(nxt, next);  // staged: LDS reads only, ahead of their use
-
-    // the delta rule step (:167-185): h *= decay; v' = (v - h k^) beta; h += k^ v'; o = h q^
-    const float decay = cur.decay, beta = cur.beta;
-    float o[RPT];
+  // the delta rule step (:167-185): h *= decay; v' = (v - h k^) beta; h += k^ v'; o = h q^
+  auto delta_step = [&](const NodeIn<E, RPT, IS>& nd, float (&o)[RPT]) {
+    const float decay = nd.decay, beta = nd.beta;
 #pragma unroll
     for (int s = 0; s < RPT; ++s) {
       float hk = 0.f;
 #pragma unroll
-      for (int e = 0; e < E; ++e) hk = fmaf(h[s][e], cur.k[e], hk);
+      for (int e = 0; e < E; ++e) hk = fmaf(h[s][e], nd.k[e], hk);
       hk = e4::group_sum<C>(hk);
-      const float dv = (Tin::to_f32(cur.v[s]) - hk * decay) * beta;
+      const float dv = (Tin::to_f32(nd.v[s]) - hk * decay) * beta;
       float hq = 0.f;
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        h[s][e] = fmaf(cur.k[e], dv, h[s][e] * decay);
-        hq = fmaf(h[s][e], cur.q[e], hq);
+        h[s][e] = fmaf(nd.k[e], dv, h[s][e] * decay);
+        hq = fmaf(h[s][e], nd.q[e], hq);
       }
       o[s] = e4::group_sum<C>(hq);
     }
-    const int64_t t = bos + u;
-    if (u < TS) {  // every lane of a row holds its sum: all write it (no lane branch in the walk)
+  };
+  // a node's snapshot from the registers, to element offset off of the buffer (a real slot)
+  auto store_snap = [&](int64_t off) {
+    SS* dst = snap + off + head_off;
+    if (full_tile && snap_nt) {
+      const __amdgpu_buffer_rsrc_t r = e4walk::buffer_rsrc(dst, a.V * K * static_cast<int>(sizeof(SS)));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+          e4walk::store4_buf<Tsnap, 2>(r, (rows[s] * K + 4 * c + 4 * C * j) * static_cast<int>(sizeof(SS)), &h[s][4 * j]);
+    } else if (full_tile) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+          store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+          if (rows[s] < a.V) store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
+    }
+  };
+  // The state the node after u starts from, depth first (pl: u's plan): park u's state when it has several children;
+  // a first child continues from the registers (rounded through the snapshot dtype, as a reload would give it); a
+  // later child pops its parent's parked state, or reloads the parent's snapshot when the stack was full.
+  int sp = 0;
+  uint64_t unparked = 0;  // nodes with several children that found the stack full
+  auto dfs_hand_over = [&](int u, int next, int pl) {
+    if ((pl & kPlanMulti) != 0) {
+      if (sp < S) {
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            float4 w = make_float4(h[s][4 * j], h[s][4 * j + 1], h[s][4 * j + 2], h[s][4 * j + 3]);
+            if constexpr (!kExact)
+              w = make_float4(e4::round_through<Tsnap>(w.x), e4::round_through<Tsnap>(w.y),
+                              e4::round_through<Tsnap>(w.z), e4::round_through<Tsnap>(w.w));
+            my_stack[sp][s * NJ + j][lane] = w;
+          }
+        ++sp;
+      } else {
+        unparked |= 1ull << u;
+      }
+    }
+    if ((pl & kPlanFirst) != 0) {
+      if constexpr (!kExact) {
+        if (!(a.skip_chain_reload && next == u + 1)) {  // an fp32 chain child keeps the registers
+#pragma unroll
+          for (int s = 0; s < RPT; ++s)
+#pragma unroll
+            for (int e = 0; e < E; ++e) h[s][e] = e4::round_through<Tsnap>(h[s][e]);
+        }
+      }
+    } else {
+      const int p = readlane(par, next);
+      if ((unparked >> p) & 1) {
+        const int64_t pslot = a.row_slots ? static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), p)) : cache_idx;
+        reload(snap_at(pslot, p));
+      } else {
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const float4 w = my_stack[sp - 1][s * NJ + j][lane];
+            h[s][4 * j] = w.x;
+            h[s][4 * j + 1] = w.y;
+            h[s][4 * j + 2] = w.z;
+            h[s][4 * j + 3] = w.w;
+          }
+        if ((pl & kPlanLast) != 0) --sp;
+      }
+    }
+  };
+
+  NodeIn<E, RPT, IS> cur, nxt;
+  // (lanes holding at most 8 state values per row: the latency-bound small grids at K = 128 and the small heads; with
+  // 16 values the second input set and state copy would cost the store-bound large grids a wave per SIMD)
+  if (kFastWalk && dfs && T <= TS && full_tile) {
+    // The common request: depth first, every node staged, every row of the tile present, so a node decides nothing
+    // but what its plan word says. Two nodes per trip with the two input sets' roles swapped: the next node's inputs
+    // are read from LDS into the idle set ahead of their use and never copied.
+    auto step = [&](int& u, const NodeIn<E, RPT, IS>& cu, NodeIn<E, RPT, IS>& nx) {
+      const int pl = readlane(plan, u);
+      int next = plan_next(pl);
+      if (next >= T) next = -1;  // (never: plan rows are the request's)
+      // This node's inputs (read one node ago) have landed by now: settling them before the next node's reads are
+      // issued lets those stay in flight through this node's math (LDS returns in order, so a wait placed after them
+      // would wait for them too). The reads are unconditional (the last node reads row 0 again), so no path joins
+      // with a different count of reads in flight.
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      fetch_staged(nx, next >= 0 ? next : 0);
+      float o[RPT];
+      delta_step(cu, o);
 #pragma unroll
       for (int s = 0; s < RPT; ++s) s_out[u][lrow[s]] = o[s];
-    } else if (c == 0) {
-#pragma unroll
-      for (int s = 0; s < RPT; ++s)
-        if (rows[s] < a.V) e4::store_scalar(a.out, t * a.stride_o + static_cast<int64_t>(hv) * a.V + rows[s], a.out_dtype, o[s]);
+      store_snap(static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_off), u)));
+      if (next >= 0) dfs_hand_over(u, next, pl);
+      u = next;
+    };
+    fetch_staged(cur, 0);
+    int u = 0;
+    for (int it = 0;;) {  // T nodes: the plan's last node has no next (and the count bounds a malformed plan)
+      step(u, cur, nxt);
+      if (u < 0 || ++it >= T) break;
+      step(u, nxt, cur);
+      if (u < 0 || ++it >= T) break;
     }
-    int64_t off = -1;  // the node's snapshot, elements from snap before head_off
-    if (a.row_slots && dfs) {
-      off = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_off), u));
-    } else {
-      int64_t slot = cache_idx;
-      if (a.row_slots) {
-        slot = uni64(e4::ld(a.snap_indices, n, u));
-        settle_loads();
-      }
-      if (slot > a.pad_slot_id) off = slot * a.stride_snap_slot + static_cast<int64_t>(u) * a.stride_snap_row;
-    }
-    if (off >= 0) {
-      SS* dst = snap + off + head_off;
-      if (full_tile && snap_nt) {
-        const __amdgpu_buffer_rsrc_t r = e4walk::buffer_rsrc(dst, a.V * K * static_cast<int>(sizeof(SS)));
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int s = 0; s < RPT; ++s)
-            e4walk::store4_buf<Tsnap, 2>(r, (rows[s] * K + 4 * c + 4 * C * j) * static_cast<int>(sizeof(SS)), &h[s][4 * j]);
-      } else if (full_tile) {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int s = 0; s < RPT; ++s)
-            store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
-      } else {
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-          for (int s = 0; s < RPT; ++s)
-            if (rows[s] < a.V) store4<Tsnap>(dst + static_cast<int64_t>(rows[s]) * K + 4 * c + 4 * C * j, &h[s][4 * j]);
-      }
-    }
-
-    // the state the next node starts from
-    if (next >= 0) {
+  } else {
+    fetch(cur, 0);
+    int u = 0;
+    for (int it = 0; it < T; ++it) {
+      // the next node and where its state comes from
+      int next = -1, pl = 0;
       if (dfs) {
-        if ((pl & kPlanMulti) != 0) {  // several children: park the state (as a reload would give it) for the later ones
-          if (sp < S) {
-#pragma unroll
-            for (int s = 0; s < RPT; ++s)
-#pragma unroll
-              for (int j = 0; j < NJ; ++j) {
-                float4 w = make_float4(h[s][4 * j], h[s][4 * j + 1], h[s][4 * j + 2], h[s][4 * j + 3]);
-                if constexpr (!kExact)
-                  w = make_float4(e4::round_through<Tsnap>(w.x), e4::round_through<Tsnap>(w.y),
-                                  e4::round_through<Tsnap>(w.z), e4::round_through<Tsnap>(w.w));
-                my_stack[sp][s * NJ + j][lane] = w;
-              }
-            ++sp;
-          } else {
-            unparked |= 1ull << u;
-          }
-        }
-        if (next_first) {
-          if constexpr (!kExact) {
-            if (!(a.skip_chain_reload && next == u + 1)) {  // an fp32 chain child keeps the registers
-#pragma unroll
-              for (int s = 0; s < RPT; ++s)
-#pragma unroll
-                for (int e = 0; e < E; ++e) h[s][e] = e4::round_through<Tsnap>(h[s][e]);
-            }
-          }
-        } else {
-          const int p = readlane(par, next);
-          if ((unparked >> p) & 1) {
-            const int64_t pslot = a.row_slots ? static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_slot), p)) : cache_idx;
-            reload(snap_at(pslot, p));
-          } else {
-#pragma unroll
-            for (int s = 0; s < RPT; ++s)
-#pragma unroll
-              for (int j = 0; j < NJ; ++j) {
-                const float4 w = my_stack[sp - 1][s * NJ + j][lane];
-                h[s][4 * j] = w.x;
-                h[s][4 * j + 1] = w.y;
-                h[s][4 * j + 2] = w.z;
-                h[s][4 * j + 3] = w.w;
-              }
-            if (next_last) --sp;
-          }
-        }
-      } else {
-        // the reference's rule (:312-329)
-        const int p = uni(static_cast<int>(e4::ld(a.parents, n, next)));
-        const int64_t pslot = a.row_slots && p >= 0 ? uni64(e4::ld(a.snap_indices, n, p)) : cache_idx;
-        bool re = p >= 0 && pslot > a.pad_slot_id;
-        if (a.skip_chain_reload) re = re && p != next - 1;
-        if (re) reload(snap_at(pslot, p));
+        pl = readlane(plan, u);
+        next = plan_next(pl);
+        if (next >= T) next = -1;  // (never: plan rows are the request's)
+      } else if (u + 1 < T) {
+        next = u + 1;
       }
-      if (next < TS)
-        cur = nxt;
-      else
-        fetch(cur, next);
+      if (next >= 0 && next < TS) fetch(nxt, next);  // staged: LDS reads only, ahead of their use
+
+      float o[RPT];
+      delta_step(cur, o);
+      const int64_t t = bos + u;
+      if (u < TS) {  // every lane of a row holds its sum: all write it (no lane branch in the walk)
+#pragma unroll
+        for (int s = 0; s < RPT; ++s) s_out[u][lrow[s]] = o[s];
+      } else if (c == 0) {
+#pragma unroll
+        for (int s = 0; s < RPT; ++s)
+          if (rows[s] < a.V) e4::store_scalar(a.out, t * a.stride_o + static_cast<int64_t>(hv) * a.V + rows[s], a.out_dtype, o[s]);
+      }
+      int64_t off = -1;  // the node's snapshot, elements from snap before head_off
+      if (a.row_slots && dfs) {
+        off = static_cast<int64_t>(readlane64(static_cast<uint64_t>(my_off), u));
+      } else {
+        int64_t slot = cache_idx;
+        if (a.row_slots) {
+          slot = uni64(e4::ld(a.snap_indices, n, u));
+          settle_loads();
+        }
+        if (slot > a.pad_slot_id) off = slot * a.stride_snap_slot + static_cast<int64_t>(u) * a.stride_snap_row;
+      }
+      if (off >= 0) store_snap(off);
+
+      // the state the next node starts from
+      if (next >= 0) {
+        if (dfs) {
+          dfs_hand_over(u, next, pl);
+        } else {
+          // the reference's rule (:312-329)
+          const int p = uni(static_cast<int>(e4::ld(a.parents, n, next)));
+          const int64_t pslot = a.row_slots && p >= 0 ? uni64(e4::ld(a.snap_indices, n, p)) : cache_idx;
+          bool re = p >= 0 && pslot > a.pad_slot_id;
+          if (a.skip_chain_reload) re = re && p != next - 1;
+          if (re) reload(snap_at(pslot, p));
+        }
+        if (next < TS)
+          cur = nxt;
+        else
+          fetch(cur, next);
+      }
+      u = next;
     }
-    u = next;
   }
   // the staged nodes' outputs: each wave its own rows (written above by this wave; in-order LDS), node-major
   for (int i = lane; i < ts * ROWS_WAVE; i += 64) {
