@@ -58,7 +58,7 @@ E4_DEV void item_of(int id, int HV, int tiles, int& n, int& hv, int& tile) {
 // The request's first TS nodes are staged in LDS up front (q, k, the workgroup's v rows, and the node scalars), so the
 // walk itself issues no global loads for them: a vector load in the walk would wait for the snapshot stores before it
 // (loads and stores share the vmcnt counter), which serialises the walk on the store latency.
-template <int K, int C, int RPT, int WAVES, int S, typename Tin, typename Tsnap>
+template <int K, int C, int RPT, int WAVES, int S, bool NEED, typename Tin, typename Tsnap>
 __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_gdn_args a) {
   constexpr int E = K / C;
   constexpr int NJ = E / 4;
@@ -155,8 +155,9 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
 
   // The walk plan (walk_plan.h), built by wave 0 and read by every wave after the staging barrier. Depth first needs
   // reloads that return the parent's own snapshot: parents before children, every row a real slot, no two rows one.
-  // Children go in increasing (need, index), except with 16-bit snapshots and the chain-child rule, where a chain
-  // child must be the first child (it continues unrounded from the registers), so that case keeps the index order.
+  // Children go in increasing (need, index) (NEED), except with 16-bit snapshots and the chain-child rule, where a
+  // chain child must be the first child (it continues unrounded from the registers), so that case keeps the index
+  // order, as do the launches without NEED.
   if (wave == 0) {
     bool ok = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
     if (ok) {
@@ -164,7 +165,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
       if (a.row_slots) bad = bad || slot_repeats(static_cast<uint64_t>(my_slot), lane, T);
       ok = __ballot(bad) == 0;
     }
-    ps.plan[lane] = ok ? build_plan(ps, lane, T, par, kExact || !a.skip_chain_reload) : kNoNext;
+    ps.plan[lane] = ok ? build_plan(ps, lane, T, par, NEED && (kExact || !a.skip_chain_reload)) : kNoNext;
     if (lane == 0) ps.dfs = ok ? 1 : 0;
   }
 
@@ -459,26 +460,26 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   }
 }
 
-template <int K, int C, int RPT, int WAVES, int S, typename Tin>
+template <int K, int C, int RPT, int WAVES, int S, bool NEED, typename Tin>
 int launch_snap(const eagle4_gdn_args& a, hipStream_t s) {
   constexpr int ROWS = WAVES * RPT * (64 / C);
   const dim3 grid(e4::ceil_div(a.V, ROWS) * a.HV * a.N);
   if (a.snap_dtype == EAGLE4_F32)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_BF16)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_F16)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
   else
     return EAGLE4_NOT_COVERED;
   return E4_LAUNCH_STATUS();
 }
 
-template <int K, int C, int RPT, int WAVES, int S>
+template <int K, int C, int RPT, int WAVES, int S, bool NEED = true>
 int launch_in(const eagle4_gdn_args& a, hipStream_t s) {
-  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, WAVES, S, e4::Bf16>(a, s);
-  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, WAVES, S, e4::F16>(a, s);
-  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, WAVES, S, e4::F32>(a, s);
+  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::Bf16>(a, s);
+  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::F16>(a, s);
+  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::F32>(a, s);
   return EAGLE4_NOT_COVERED;
 }
 
@@ -508,7 +509,10 @@ extern "C" int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* a, void* 
       // lane's K values) halve and the grid doubles. Batch 1 24.3 -> 21.7 us, batch 2 25.2 -> 24.3 us; from batch 4
       // up (4 x 32 x 4 workgroups) the 8-lane form is faster (batch 64: 375 against 396 us).
       const int64_t groups8 = e4::ceil_div(a->V, 32) * static_cast<int64_t>(a->HV) * a->N;
-      if (groups8 <= 256) return launch_in<128, 16, 1, 4, 2>(*a, s);
+      // These grids' walks are latency-bound and the need order is the plan's longest part (depths by pointer
+      // jumping, then a pass per tree level): they walk children in index order and park up to four states instead
+      // of two, enough for the nesting of index order in drafted trees; a parent beyond them reloads its snapshot.
+      if (groups8 <= 256) return launch_in<128, 16, 1, 4, 4, false>(*a, s);
       return launch_in<128, 8, 1, 4, 2>(*a, s);
     }
     case 256: return launch_in<256, 16, 1, 4, 2>(*a, s);

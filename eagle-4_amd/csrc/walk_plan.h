@@ -99,7 +99,8 @@ E4_DEV int build_plan(PlanScratch& ps, int lane, int T, int par, bool by_need) {
   if (child) atomicOr(reinterpret_cast<unsigned long long*>(&ps.kids[par]), 1ull << lane);
   wave_lds_order();
 
-  int need = 0;
+  uint64_t kids;
+  int first, after = -1;  // first child; the sibling walked after row u
   if (by_need) {
     // depths: d(u) += d(up(u)); up(u) = up(up(u)) until every row points at the root (six rounds reach 64 levels)
     int dep = child ? 1 : 0, up = child ? par : lane;
@@ -115,6 +116,7 @@ E4_DEV int build_plan(PlanScratch& ps, int lane, int T, int par, bool by_need) {
       const int cand = deepest | (1 << b);
       if (__ballot(lane < T && dep >= cand) != 0) deepest = cand;
     }
+    int need = 0;
     for (int level = deepest; level >= 1; --level) {
       const bool mine = child && dep == level;
       if (__ballot(mine) == 0) continue;
@@ -124,26 +126,34 @@ E4_DEV int build_plan(PlanScratch& ps, int lane, int T, int par, bool by_need) {
       }
       wave_lds_order();
     }
-  }
-  const int key = (by_need ? need * 64 : 0) + lane;
-  ps.key[lane] = key;
-  if (child) atomicMin(&ps.first[par], key);
-  wave_lds_order();
+    const int key = need * 64 + lane;
+    ps.key[lane] = key;
+    if (child) atomicMin(&ps.first[par], key);
+    wave_lds_order();
 
-  const uint64_t kids = ps.kids[lane];
-  const int fk = ps.first[lane];
-  const int first = fk == 0x7fffffff ? -1 : (fk & 63);
-  int after = -1;  // the sibling walked after row u: the smallest key above u's among its parent's children
-  if (child) {
-    uint64_t sib = ps.kids[par] & ~(1ull << lane);
-    int best = 0x7fffffff;
-    while (sib != 0) {
-      const int s = __builtin_ctzll(sib);
-      sib &= sib - 1;
-      const int ks = ps.key[s];
-      if (ks > key && ks < best) best = ks;
+    kids = ps.kids[lane];
+    const int fk = ps.first[lane];
+    first = fk == 0x7fffffff ? -1 : (fk & 63);
+    if (child) {  // the smallest key above u's among its parent's children
+      uint64_t sib = ps.kids[par] & ~(1ull << lane);
+      int best = 0x7fffffff;
+      while (sib != 0) {
+        const int s = __builtin_ctzll(sib);
+        sib &= sib - 1;
+        const int ks = ps.key[s];
+        if (ks > key && ks < best) best = ks;
+      }
+      after = best == 0x7fffffff ? -1 : (best & 63);
     }
-    after = best == 0x7fffffff ? -1 : (best & 63);
+  } else {
+    // index order: the first child is the lowest bit of the row's child mask, the next sibling the lowest bit of the
+    // parent's mask above the row (2 << 63 wraps to 0: row 63 has none above it)
+    kids = ps.kids[lane];
+    first = kids != 0 ? __builtin_ctzll(kids) : -1;
+    if (child) {
+      const uint64_t above = ps.kids[par] & ~((2ull << lane) - 1ull);
+      after = above != 0 ? __builtin_ctzll(above) : -1;
+    }
   }
   // A row without children continues at the next sibling of its nearest ancestor-or-self that has one (the root:
   // the walk ends). Pointer jumping to the first marked ancestor-or-self, marked rows pointing at themselves.

@@ -92,14 +92,18 @@ NESTED = [-1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 0, 1, 2, 3, 4, 5]
 
 
 # A complete binary tree: walked neediest-child-last (fp32 snapshots) it needs three parked states, one more than the
-# stack holds, so the deepest branch points reload their snapshots.
+# two that the large grids' walk holds, so the deepest branch points reload their snapshots there.
 BINARY = [-1] + [(i - 1) // 2 for i in range(1, 16)]
 
 
+# Value heads: 4 is a small grid (16 lanes per row, children in index order, four parked states), 64 a large one
+# (8 lanes per row, children in need order, two parked states).
+@pytest.mark.parametrize("value_heads", [4, 64])
 @pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
-def test_nested_branches_beyond_the_parked_states(dev, state_dtype):
-    announce(f"recurrence nested branches {state_dtype}")
-    _vllm_case(dev, [NESTED, BINARY, _random_tree(16, 4), [-1] + [0] * 15], (2, 4, 128, 128), state_dtype=state_dtype)
+def test_nested_branches_beyond_the_parked_states(dev, state_dtype, value_heads):
+    announce(f"recurrence nested branches {state_dtype} HV {value_heads}")
+    _vllm_case(dev, [NESTED, BINARY, _random_tree(16, 4), [-1] + [0] * 15], (2, value_heads, 128, 128),
+               state_dtype=state_dtype)
 
 
 COMB = [-1] + [2 * ((i - 1) // 2) for i in range(1, 64)]  # even rows a 32-row spine, every spine row with a leaf too

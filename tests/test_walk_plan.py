@@ -69,20 +69,27 @@ def emulate_build_plan(parents: list[int], by_need: bool) -> list[int]:
                 need[u] = _need_of(hist[u])
             for u in rows:  # atomicAdd(hist[par], 1 << 8 * need)
                 hist[par[u]] += 1 << (8 * int(need[u]))
-    key = (need * 64 if by_need else 0) + lane
-    for u in np.flatnonzero(child):  # atomicMin(first[par], key)
-        first_key[par[u]] = min(first_key[par[u]], int(key[u]))
-    first = np.array([-1 if fk == 0x7FFFFFFF else fk & 63 for fk in first_key])
-    after = np.full(LANES, -1)
-    for u in np.flatnonzero(child):
-        best = 0x7FFFFFFF
-        sib = kids[par[u]] & ~(1 << int(u))
-        while sib:
-            s = (sib & -sib).bit_length() - 1
-            sib &= sib - 1
-            if key[u] < key[s] < best:
-                best = int(key[s])
-        after[u] = -1 if best == 0x7FFFFFFF else best & 63
+    if by_need:
+        key = need * 64 + lane
+        for u in np.flatnonzero(child):  # atomicMin(first[par], key)
+            first_key[par[u]] = min(first_key[par[u]], int(key[u]))
+        first = np.array([-1 if fk == 0x7FFFFFFF else fk & 63 for fk in first_key])
+        after = np.full(LANES, -1)
+        for u in np.flatnonzero(child):
+            best = 0x7FFFFFFF
+            sib = kids[par[u]] & ~(1 << int(u))
+            while sib:
+                s = (sib & -sib).bit_length() - 1
+                sib &= sib - 1
+                if key[u] < key[s] < best:
+                    best = int(key[s])
+            after[u] = -1 if best == 0x7FFFFFFF else best & 63
+    else:  # index order from the masks' lowest bits: the first child, the next sibling above the row (64-bit masks)
+        first = np.array([(k & -k).bit_length() - 1 if k else -1 for k in kids])
+        after = np.full(LANES, -1)
+        for u in np.flatnonzero(child):
+            above = kids[par[u]] & ~(((2 << int(u)) - 1) & (2**64 - 1)) & (2**64 - 1)
+            after[u] = (above & -above).bit_length() - 1 if above else -1
     marked = (lane == 0) | (lane >= T) | (after >= 0)
     J = np.where(marked, lane, par)
     for _ in range(6):
