@@ -58,7 +58,7 @@ E4_DEV void item_of(int id, int HV, int tiles, int& n, int& hv, int& tile) {
 // The request's first TS nodes are staged in LDS up front (q, k, the workgroup's v rows, and the node scalars), so the
 // walk itself issues no global loads for them: a vector load in the walk would wait for the snapshot stores before it
 // (loads and stores share the vmcnt counter), which serialises the walk on the store latency.
-template <int K, int C, int RPT, int WAVES, int S, bool NEED, typename Tin, typename Tsnap>
+template <int K, int C, int RPT, int WAVES, int S, bool SMALL, typename Tin, typename Tsnap>
 __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_gdn_args a) {
   constexpr int E = K / C;
   constexpr int NJ = E / 4;
@@ -120,7 +120,11 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   // A launch whose snapshots outgrow the last-level cache (MI355X: 256 MB) stores them nontemporally: regular stores
   // leave a cache's worth of dirty lines that the next kernel's reads pay to write back (a 512 MB stream: 13 us
   // faster to store, 39 us slower for the kernel after it). The launch's bytes from the grid and this request's nodes.
-  const bool snap_nt = static_cast<int64_t>(gridDim.x) * ROWS * K * static_cast<int64_t>(sizeof(SS)) * T > (256ll << 20);
+  // The small grids (SMALL) store nontemporally too: their walk is latency-bound and its regular stores' dirty L2
+  // lines are written back before the kernel counts as finished (batch 1: 13.0 -> 11.8 us, batch 2: 16.6 -> 15.9;
+  // batches 4 and 8, on the 8-lane form, are 5-7 % slower with nontemporal stores).
+  const bool snap_nt =
+      SMALL || static_cast<int64_t>(gridDim.x) * ROWS * K * static_cast<int64_t>(sizeof(SS)) * T > (256ll << 20);
   if (T <= 0) return;
 
   // Lane i holds row i's parent and slot (rows of at most 64-row requests).
@@ -155,9 +159,9 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
 
   // The walk plan (walk_plan.h), built by wave 0 and read by every wave after the staging barrier. Depth first needs
   // reloads that return the parent's own snapshot: parents before children, every row a real slot, no two rows one.
-  // Children go in increasing (need, index) (NEED), except with 16-bit snapshots and the chain-child rule, where a
-  // chain child must be the first child (it continues unrounded from the registers), so that case keeps the index
-  // order, as do the launches without NEED.
+  // Children go in increasing (need, index), except with 16-bit snapshots and the chain-child rule, where a chain
+  // child must be the first child (it continues unrounded from the registers), so that case keeps the index order,
+  // as do the small grids (SMALL).
   if (wave == 0) {
     bool ok = T <= 64 && (a.row_slots ? true : (cache_idx > a.pad_slot_id && a.stride_snap_row != 0));
     if (ok) {
@@ -165,7 +169,7 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
       if (a.row_slots) bad = bad || slot_repeats(static_cast<uint64_t>(my_slot), lane, T);
       ok = __ballot(bad) == 0;
     }
-    ps.plan[lane] = ok ? build_plan(ps, lane, T, par, NEED && (kExact || !a.skip_chain_reload)) : kNoNext;
+    ps.plan[lane] = ok ? build_plan(ps, lane, T, par, !SMALL && (kExact || !a.skip_chain_reload)) : kNoNext;
     if (lane == 0) ps.dfs = ok ? 1 : 0;
   }
 
@@ -460,26 +464,26 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_tree_walk_kernel(const eagle4_
   }
 }
 
-template <int K, int C, int RPT, int WAVES, int S, bool NEED, typename Tin>
+template <int K, int C, int RPT, int WAVES, int S, bool SMALL, typename Tin>
 int launch_snap(const eagle4_gdn_args& a, hipStream_t s) {
   constexpr int ROWS = WAVES * RPT * (64 / C);
   const dim3 grid(e4::ceil_div(a.V, ROWS) * a.HV * a.N);
   if (a.snap_dtype == EAGLE4_F32)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, SMALL, Tin, e4::F32><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_BF16)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, SMALL, Tin, e4::Bf16><<<grid, 64 * WAVES, 0, s>>>(a);
   else if (a.snap_dtype == EAGLE4_F16)
-    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, NEED, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
+    gdn_tree_walk_kernel<K, C, RPT, WAVES, S, SMALL, Tin, e4::F16><<<grid, 64 * WAVES, 0, s>>>(a);
   else
     return EAGLE4_NOT_COVERED;
   return E4_LAUNCH_STATUS();
 }
 
-template <int K, int C, int RPT, int WAVES, int S, bool NEED = true>
+template <int K, int C, int RPT, int WAVES, int S, bool SMALL = false>
 int launch_in(const eagle4_gdn_args& a, hipStream_t s) {
-  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::Bf16>(a, s);
-  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::F16>(a, s);
-  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, WAVES, S, NEED, e4::F32>(a, s);
+  if (a.in_dtype == EAGLE4_BF16) return launch_snap<K, C, RPT, WAVES, S, SMALL, e4::Bf16>(a, s);
+  if (a.in_dtype == EAGLE4_F16) return launch_snap<K, C, RPT, WAVES, S, SMALL, e4::F16>(a, s);
+  if (a.in_dtype == EAGLE4_F32) return launch_snap<K, C, RPT, WAVES, S, SMALL, e4::F32>(a, s);
   return EAGLE4_NOT_COVERED;
 }
 
@@ -511,8 +515,9 @@ extern "C" int eagle4_gdn_tree_recurrent_update(const eagle4_gdn_args* a, void* 
       const int64_t groups8 = e4::ceil_div(a->V, 32) * static_cast<int64_t>(a->HV) * a->N;
       // These grids' walks are latency-bound and the need order is the plan's longest part (depths by pointer
       // jumping, then a pass per tree level): they walk children in index order and park up to four states instead
-      // of two, enough for the nesting of index order in drafted trees; a parent beyond them reloads its snapshot.
-      if (groups8 <= 256) return launch_in<128, 16, 1, 4, 4, false>(*a, s);
+      // of two, enough for the nesting of index order in drafted trees (a parent beyond them reloads its snapshot),
+      // and store their snapshots nontemporally.
+      if (groups8 <= 256) return launch_in<128, 16, 1, 4, 4, true>(*a, s);
       return launch_in<128, 8, 1, 4, 2>(*a, s);
     }
     case 256: return launch_in<256, 16, 1, 4, 2>(*a, s);
