@@ -253,7 +253,8 @@ void tree_conv_kernel(const eagle4_conv_args a, const Lds off) {
       }
       uint16_t* op = out + t * a.stride_o_token + c0 * a.stride_o_dim;
       if (ovec) {
-        *reinterpret_cast<uint4*>(op) = make_uint4(o[0], o[1], o[2], o[3]);
+        typedef uint32_t u32x4o __attribute__((ext_vector_type(4)));
+        __builtin_nontemporal_store(u32x4o{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4o*>(op));
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e)

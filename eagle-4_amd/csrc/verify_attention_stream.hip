@@ -622,10 +622,10 @@ E4_DEV void store_piece(const f32x4_t (&acc)[D / 16], float ls, float mref, bool
   for (int dt = 0; dt < D / 16; ++dt) {
     const f32x4_t v = acc[dt] * inv;
     __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])}, ro,
-                                          ooff + 2 * (16 * dt + 4 * g), 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, poff + 4 * (16 * dt + 4 * g), 0, 0);
+                                          ooff + 2 * (16 * dt + 4 * g), 0, 2);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rp, poff + 4 * (16 * dt + 4 * g), 0, 2);
   }
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl, loff, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse), rl, loff, 0, 2);
 }
 
 constexpr int waves_per_eu(int d) { return d == 256 ? 2 : (d == 128 ? 3 : 4); }
