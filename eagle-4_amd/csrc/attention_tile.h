@@ -13,6 +13,8 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));  // a 16-byte MFMA operand as a native vector
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
+// Splits whose partials a merge thread loads at once (the split-schedule, fp32 and draft-row merges).
+constexpr int kMergeGroup = 8;
 constexpr int kTileKeys = 32;
 
 template <typename T>

@@ -227,16 +227,36 @@ __global__ __launch_bounds__(256) void row_merge_kernel(const eagle4_row_attn_ar
   const int head = static_cast<int>(pair % a.heads);
   const int64_t b = row / a.rows_per_request, t = row % a.rows_per_request;
   const int64_t part0 = ((b * a.heads + head) * (a.splits + 1)) * a.rows_padded + t;
+  // The splits in groups of kMergeGroup, every load of a group issued before the first is used (one memory round trip
+  // per group, not per split; a group's loads past the last split re-read the first), the same operations in the same
+  // order as one split at a time.
   float top = -INFINITY;
-  for (int s = 0; s < splits; ++s) top = fmaxf(top, a.part_lse[part0 + s * a.rows_padded]);
+  for (int s0 = 0; s0 < splits; s0 += kMergeGroup) {
+    float l[kMergeGroup];
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i) l[i] = a.part_lse[part0 + (s0 + i < splits ? s0 + i : s0) * a.rows_padded];
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i)
+      if (s0 + i < splits) top = fmaxf(top, l[i]);
+  }
   float wsum = 0.f;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < splits; ++s) {
-    const int64_t part = part0 + s * a.rows_padded;
-    const float lse = a.part_lse[part];
-    const float w = lse == -INFINITY ? 0.f : exp2f(lse - top);
-    wsum += w;
-    if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t*>(a.part_out + part * D + d);
+  for (int s0 = 0; s0 < splits; s0 += kMergeGroup) {
+    float l[kMergeGroup];
+    f32x4_t v[kMergeGroup];
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i) {
+      const int64_t part = part0 + (s0 + i < splits ? s0 + i : s0) * a.rows_padded;
+      l[i] = a.part_lse[part];
+      v[i] = *reinterpret_cast<const f32x4_t*>(a.part_out + part * D + d);
+    }
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i) {
+      if (s0 + i >= splits) break;
+      const float w = l[i] == -INFINITY ? 0.f : exp2f(l[i] - top);
+      wsum += w;
+      if (w != 0.f) acc += w * v[i];
+    }
   }
   uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.stride_o_row + static_cast<int64_t>(head) * a.stride_o_head + d;
   const uint32_t lo = T::from_f32(acc.x / wsum) | (static_cast<uint32_t>(T::from_f32(acc.y / wsum)) << 16);

@@ -244,20 +244,41 @@ __global__ __launch_bounds__(256) void verify_f32_merge(const eagle4_attn_args a
   const int nrow = row_tiles * 16;
   const float* lse = a.workspace + static_cast<int64_t>(a.num_reqs) * a.Hkv * max_splits * nrow * D;
   const int64_t part0 = (static_cast<int64_t>(b) * a.Hkv + kvh) * max_splits * nrow + rho;
+  // The splits in groups of kMergeGroup, every load of a group issued before the first is used (one memory round trip
+  // per group, not per split; a group's loads past the last split re-read the first), the same operations in the same
+  // order as one split at a time.
+  const int ns = rq.splits;
   float mx = -INFINITY;
-  for (int s = 0; s < rq.splits; ++s) mx = fmaxf(mx, lse[part0 + static_cast<int64_t>(s) * nrow]);
+  for (int s0 = 0; s0 < ns; s0 += kMergeGroup) {
+    float l[kMergeGroup];
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i) l[i] = lse[part0 + static_cast<int64_t>(s0 + i < ns ? s0 + i : s0) * nrow];
+#pragma unroll
+    for (int i = 0; i < kMergeGroup; ++i)
+      if (s0 + i < ns) mx = fmaxf(mx, l[i]);
+  }
   float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
   float wsum = 0.f;
   if (mx != -INFINITY) {
-    for (int s = 0; s < rq.splits; ++s) {
-      const int64_t part = part0 + static_cast<int64_t>(s) * nrow;
-      const float w = exp2f(lse[part] - mx);
-      const float4 v = *reinterpret_cast<const float4*>(a.workspace + part * D + d);
-      sum.x += w * v.x;
-      sum.y += w * v.y;
-      sum.z += w * v.z;
-      sum.w += w * v.w;
-      wsum += w;
+    for (int s0 = 0; s0 < ns; s0 += kMergeGroup) {
+      float l[kMergeGroup];
+      float4 v[kMergeGroup];
+#pragma unroll
+      for (int i = 0; i < kMergeGroup; ++i) {
+        const int64_t part = part0 + static_cast<int64_t>(s0 + i < ns ? s0 + i : s0) * nrow;
+        l[i] = lse[part];
+        v[i] = *reinterpret_cast<const float4*>(a.workspace + part * D + d);
+      }
+#pragma unroll
+      for (int i = 0; i < kMergeGroup; ++i) {
+        if (s0 + i >= ns) break;
+        const float w = exp2f(l[i] - mx);
+        sum.x += w * v[i].x;
+        sum.y += w * v[i].y;
+        sum.z += w * v[i].z;
+        sum.w += w * v[i].w;
+        wsum += w;
+      }
     }
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
